@@ -1,0 +1,186 @@
+#!/usr/bin/env python3
+"""Throughput of the DINOv3 ViT-S+/16 forward pass on one MI355X.
+
+A step is one resident hipGraph replay of the full 12-block forward over one
+batch of synthetic images already in HBM (the scope of the reference's
+ForwardTimings, engine.rs:272): float32 NCHW pixels in, float32
+[batch, 201, 384] tokens out. The headline workload is BASELINE.json's
+config 3 (batch 64 at 224x224); batch 32 (config 2) is reported beside it.
+Weights are the seeded BASELINE random init; inputs are seeded N(0, 1).
+
+Prints one JSON line with the metric, the roofline of the dominant kernel
+(device time from HIP events on the model's stream) and the float64 CPU
+oracle timed on this host as a baseline.
+"""
+import argparse
+import json
+import os
+import sys
+import tempfile
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "dinov3-loom_amd"))
+
+METRIC = "images/sec ViT-S+/16 224² at batch 32/64 on 1 MI355X; % MFMA roofline"
+PEAK_TFLOPS = 2500.0  # MI355X dense f16 MFMA
+PEAK_GBS = 8000.0  # MI355X HBM3E
+GFLOP_PER_IMAGE = 12.2415  # 224x224 forward, algorithmic
+
+
+def kernel_work(name, b, T, G):
+    """Algorithmic (flops, bytes) of one launch."""
+    r, P, H = b * T, G * G, 384
+    f16, f32 = 2, 4
+    if name == "patch_embed":
+        return 2 * b * P * 768 * H, b * 3 * (16 * G) ** 2 * f32 + H * 768 * f16 + r * H * f16
+    if name == "layernorm":
+        return 0, 2 * r * H * f16
+    if name == "layernorm_f32":
+        return 0, r * H * (f16 + f32)
+    if name == "qkv_rope":
+        return 2 * r * H * 3 * H, r * H * f16 + 3 * H * H * f16 + 3 * r * H * f16
+    if name == "attention":
+        return 4 * b * 6 * T * T * 64, 4 * r * H * f16
+    if name == "resid_384":
+        return 2 * r * H * H, r * H * f16 + H * H * f16 + 2 * r * H * f16
+    if name == "resid_1536":
+        return 2 * r * 1536 * H, r * 1536 * f16 + 1536 * H * f16 + 2 * r * H * f16
+    if name == "swiglu":
+        return 2 * r * H * 3072, r * H * f16 + 3072 * H * f16 + r * 1536 * f16
+    if name == "splitk":
+        return 2 * r * 1536 * H, r * 1536 * f16 + 1536 * H * f16 + 4 * r * H * f32
+    if name == "splitk_reduce":
+        return 0, 4 * r * H * f32 + 2 * r * H * f16
+    raise KeyError(name)
+
+
+def timed_replays(model, b, steps):
+    model.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        model.replay(b)
+    model.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def cpu_baseline(path, seconds):
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import dinov3_hrx as d
+    import oracle
+
+    oracle.set_threads(1)
+    w = oracle.Weights.from_file(path)
+    px = d.random_pixels(1, 64)
+    n, t0 = 0, time.perf_counter()
+    while n < 64:
+        oracle.forward(w, px[n], 14)
+        n += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": round(n / dt, 4), "unit": "images/s", "cores": 1, "kind": "port",
+            "sample": f"{n} image(s) of the b=64 workload at 224x224 through the float64 C oracle "
+                      f"(oracle/dinov3_oracle.c), 1 thread, {dt:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--batch", type=int, default=64)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (images shard across GPUs with no "
+              "exchange; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import dinov3_hrx as d
+
+    b = args.batch
+    with tempfile.TemporaryDirectory() as tmp:
+        path = os.path.join(tmp, "weights.safetensors")
+        d.write_random_weights(path, seed=0, preset=0)
+        model = d.DINOv3.load(path, d.Options(device=0, max_batch=max(b, 32)))
+        px = d.random_pixels(1, b)
+
+        # Pick the down-projection variant for this batch by a short trial
+        # (the reference uses the residual GEMM for b > 1, split-K at b = 1).
+        trial = {}
+        for mode in (0, 1):
+            model.set_splitk(mode)
+            model.stage(px)
+            trial[mode] = timed_replays(model, b, 10)
+        mode = min(trial, key=trial.get)
+        model.set_splitk(mode)
+        model.stage(px)
+        for _ in range(args.warmup):
+            model.replay(b)
+        sec = timed_replays(model, b, args.steps)
+        value = b / sec
+
+        # Batch 32 (config 2) on the same resident model.
+        model.stage(px[:32])
+        for _ in range(args.warmup):
+            model.replay(32)
+        sec32 = timed_replays(model, 32, args.steps)
+
+        # Per-launch device time (HIP events on the model's stream).
+        launches = model.launch_timings(b, iters=20, splitk=mode)
+        kernels = {}
+        for i, (name, ms) in enumerate(launches):
+            if name == "resid":
+                # the o-projection (k = 384) precedes the down projection (k = 1536) in each block
+                name = "resid_1536" if launches[i - 1][0] == "swiglu" else "resid_384"
+            k = kernels.setdefault(name, {"count": 0, "ms": 0.0})
+            k["count"] += 1
+            k["ms"] += ms
+        T, G = 201, 14
+        table = []
+        for name, k in kernels.items():
+            flops, nbytes = kernel_work(name, b, T, G)
+            avg = k["ms"] / k["count"]
+            tf = flops / (avg * 1e-3) / 1e12
+            gbs = nbytes / (avg * 1e-3) / 1e9
+            table.append({"kernel": name, "launches": k["count"], "avg_us": round(avg * 1e3, 2),
+                          "total_us": round(k["ms"] * 1e3, 1), "tflops": round(tf, 1), "gbs": round(gbs, 1),
+                          "mfma_frac": round(tf / PEAK_TFLOPS, 4), "hbm_frac": round(gbs / PEAK_GBS, 4)})
+        table.sort(key=lambda r: -r["total_us"])
+        dom = table[0]
+        flops, nbytes = kernel_work(dom["kernel"], b, T, G)
+        ridge = PEAK_TFLOPS * 1e12 / (PEAK_GBS * 1e9)
+        if flops and flops / nbytes >= ridge:
+            roof = {"kernel": dom["kernel"], "bound": "mfma", "achieved": dom["tflops"], "peak": PEAK_TFLOPS,
+                    "unit": "TFLOP/s", "frac": round(dom["tflops"] / PEAK_TFLOPS, 4)}
+        else:
+            roof = {"kernel": dom["kernel"], "bound": "hbm", "achieved": dom["gbs"], "peak": PEAK_GBS,
+                    "unit": "GB/s", "frac": round(dom["gbs"] / PEAK_GBS, 4)}
+        roof["traffic"] = None
+        roof["avg_us"] = dom["avg_us"]
+        model.close()
+
+        cpu = None if args.no_cpu else cpu_baseline(path, args.cpu_seconds)
+
+    for row in table:
+        print(json.dumps(row), file=sys.stderr)
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "images/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(sec * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f16", "data": "synthetic",
+        "config": {"workload": f"DINOv3 ViT-S+/16 forward, 224x224, batch {b}, resident hipGraph replay "
+                               "(BASELINE.json config 3)", "batch": b, "image_size": 224, "tokens": T,
+                   "down_proj": "splitk" if mode == 1 else "resid", "weights": "seeded random init (BASELINE)"},
+        "mfma_frac_forward": round(value * GFLOP_PER_IMAGE / 1e3 / PEAK_TFLOPS, 4),
+        "batch32": {"value": round(32 / sec32, 1), "ms_per_step": round(sec32 * 1e3, 4)},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "kernels": table,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

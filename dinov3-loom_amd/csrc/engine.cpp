@@ -1,0 +1,434 @@
+// HIP runtime behind the engine-level C ABI (include/dinov3_engine.h). It
+// replaces the HRX surface used by the reference's src/engine.rs:
+// Device::open + target check (engine.rs:40-59), Stream::allocate/upload
+// (60-70, 191-202), graph record (87-129), replay (203-214), pinned readback
+// (215-269), the graph-vs-direct benchmark (130-190) and poison-on-failure.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cstring>
+#include <map>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/dinov3_engine.h"
+#include "errors.hpp"
+#include "kernels/launch.hpp"
+
+namespace {
+
+constexpr char kPoisoned[] = "session is unusable after a GPU failure";
+
+struct Recorded {
+    hipGraphExec_t exec = nullptr;
+    std::vector<dhx_launch> launches;
+};
+
+}  // namespace
+
+struct dhx_engine {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::vector<void*> buffers;
+    std::vector<uint64_t> sizes;
+    std::map<uint64_t, Recorded> graphs;
+    void* readback = nullptr;
+    uint64_t readback_bytes = 0;
+    bool failed = false;
+    bool fail_next = false;
+    std::string error;
+};
+
+namespace {
+
+// Every HIP call goes through here: a failure (or an injected one) poisons
+// the engine, as any failed HRX call does in engine.rs.
+void hip_check(dhx_engine* e, hipError_t err, const char* what) {
+    if (e->fail_next) {
+        e->fail_next = false;
+        err = hipErrorUnknown;
+    }
+    if (err != hipSuccess) {
+        e->failed = true;
+        throw dhx::Error(std::string(what) + ": " + hipGetErrorString(err));
+    }
+}
+
+void ensure_usable(const dhx_engine* e) {
+    if (e->failed) throw dhx::Error(kPoisoned);
+}
+
+void* region_ptr(const dhx_engine* e, const dhx_region& r) {
+    return static_cast<char*>(e->buffers[r.buffer]) + r.offset;
+}
+
+void check_region(const dhx_engine* e, const dhx_region& r) {
+    if (r.buffer >= e->buffers.size()) throw dhx::Error("region names an unknown buffer");
+    if (r.offset > e->sizes[r.buffer] || r.bytes > e->sizes[r.buffer] - r.offset)
+        throw dhx::Error("region exceeds its buffer");
+}
+
+using dhx::kHidden;
+
+struct Need {
+    uint32_t bindings;
+    std::vector<uint64_t> bytes;
+};
+
+uint64_t tokens_for(uint32_t grid) { return (uint64_t)grid * grid + dhx::kPrefix; }
+
+// The shapes each kernel reads and writes, from its scalars; recording and
+// dispatch refuse any binding smaller than this (so no kernel can run past a
+// buffer) and any misaligned binding (kernels use 16-byte vector accesses).
+Need required(const dhx_launch& l) {
+    const uint32_t* s = l.scalars;
+    const uint64_t H = kHidden;
+    auto positive = [](uint64_t v, const char* what) {
+        if (v == 0) throw dhx::Error(std::string(what) + " must be positive");
+    };
+    switch (l.kernel) {
+        case DHX_K_PATCH_EMBED: {
+            positive(s[0], "images");
+            positive(s[1], "grid");
+            const uint64_t side = 16ull * s[1], T = tokens_for(s[1]);
+            return {5, {s[0] * 3 * side * side * 4, H * 768 * 2, H * 4, 5 * H * 4, s[0] * T * H * 2}};
+        }
+        case DHX_K_LAYERNORM:
+        case DHX_K_LAYERNORM_F32: {
+            positive(s[0], "rows");
+            const uint64_t out = l.kernel == DHX_K_LAYERNORM ? 2 : 4;
+            return {4, {s[0] * H * 2, H * 4, H * 4, s[0] * H * out}};
+        }
+        case DHX_K_QKV_ROPE:
+        case DHX_K_ATTENTION: {
+            positive(s[0], "images");
+            positive(s[1], "grid");
+            const uint64_t T = tokens_for(s[1]), P = (uint64_t)s[1] * s[1];
+            if (s[2] % 128 != 0 || s[2] < T) throw dhx::Error("tpad must be a multiple of 128 covering every token");
+            const uint64_t heads = s[0] * dhx::kHeads * (uint64_t)s[2] * dhx::kHeadDim * 2;
+            if (l.kernel == DHX_K_ATTENTION) return {4, {heads, heads, heads, s[0] * T * H * 2}};
+            return {8, {s[0] * T * H * 2, 3 * H * H * 2, 3 * H * 4, P * 64 * 4, P * 64 * 4, heads, heads, heads}};
+        }
+        case DHX_K_RESID: {
+            positive(s[0], "rows");
+            if (s[1] == 0 || s[1] % 64 != 0) throw dhx::Error("k must be a positive multiple of 64");
+            return {5, {s[0] * (uint64_t)s[1] * 2, H * s[1] * 2, H * 4, H * 4, s[0] * H * 2}};
+        }
+        case DHX_K_SWIGLU:
+            positive(s[0], "rows");
+            return {4, {s[0] * H * 2, 2ull * dhx::kFF * H * 2, 2ull * dhx::kFF * 4, s[0] * (uint64_t)dhx::kFF * 2}};
+        case DHX_K_SPLITK: {
+            positive(s[0], "rows");
+            positive(s[2], "splits");
+            if (s[1] == 0 || s[1] % (64ull * s[2]) != 0) throw dhx::Error("k must split into multiples of 64");
+            return {3, {s[0] * (uint64_t)s[1] * 2, H * s[1] * 2, (uint64_t)s[2] * s[0] * H * 4}};
+        }
+        case DHX_K_SPLITK_REDUCE:
+            positive(s[0], "rows");
+            positive(s[1], "splits");
+            return {4, {(uint64_t)s[1] * s[0] * H * 4, H * 4, H * 4, s[0] * H * 2}};
+        default:
+            throw dhx::Error("unknown kernel id " + std::to_string(l.kernel));
+    }
+}
+
+void validate(const dhx_engine* e, const dhx_launch& l) {
+    const Need need = required(l);
+    if (l.n_bindings != need.bindings)
+        throw dhx::Error("kernel " + std::to_string(l.kernel) + " takes " + std::to_string(need.bindings) +
+                         " bindings, got " + std::to_string(l.n_bindings));
+    for (uint32_t i = 0; i < l.n_bindings; ++i) {
+        const dhx_region& r = l.bindings[i];
+        check_region(e, r);
+        if (r.offset % 16 != 0) throw dhx::Error("binding " + std::to_string(i) + " is not 16-byte aligned");
+        if (r.bytes < need.bytes[i])
+            throw dhx::Error("kernel " + std::to_string(l.kernel) + " binding " + std::to_string(i) + " needs " +
+                             std::to_string(need.bytes[i]) + " bytes, region has " + std::to_string(r.bytes));
+    }
+}
+
+hipError_t launch_one(dhx_engine* e, const dhx_launch& l) {
+    using namespace dhx;
+    auto P = [&](int i) { return region_ptr(e, l.bindings[i]); };
+    auto F = [&](int i) { return static_cast<const float*>(P(i)); };
+    auto Hf = [&](int i) { return static_cast<half_t*>(P(i)); };
+    const uint32_t* s = l.scalars;
+    switch (l.kernel) {
+        case DHX_K_PATCH_EMBED:
+            return launch_patch_embed({F(0), Hf(1), F(2), F(3), Hf(4), (int)s[0], (int)s[1]}, e->stream);
+        case DHX_K_LAYERNORM:
+        case DHX_K_LAYERNORM_F32:
+            return launch_layernorm({Hf(0), F(1), F(2), P(3), (int)s[0], l.kernel == DHX_K_LAYERNORM_F32}, e->stream);
+        case DHX_K_QKV_ROPE:
+            return launch_qkv_rope({Hf(0), Hf(1), F(2), F(3), F(4), Hf(5), Hf(6), Hf(7), (int)s[0], (int)s[1], (int)s[2]},
+                                   e->stream);
+        case DHX_K_ATTENTION:
+            return launch_attention({Hf(0), Hf(1), Hf(2), Hf(3), (int)s[0], (int)tokens_for(s[1]), (int)s[2]}, e->stream);
+        case DHX_K_RESID:
+            return launch_resid({Hf(0), Hf(1), F(2), F(3), Hf(4), (int)s[0], (int)s[1]}, e->stream);
+        case DHX_K_SWIGLU:
+            return launch_swiglu({Hf(0), Hf(1), F(2), Hf(3), (int)s[0]}, e->stream);
+        case DHX_K_SPLITK:
+            return launch_splitk({Hf(0), Hf(1), (float*)P(2), (int)s[0], (int)s[1], (int)s[2]}, e->stream);
+        case DHX_K_SPLITK_REDUCE:
+            return launch_splitk_reduce({F(0), F(1), F(2), Hf(3), (int)s[0], (int)s[1]}, e->stream);
+        default:
+            return hipErrorInvalidValue;
+    }
+}
+
+void run_list(dhx_engine* e, const std::vector<dhx_launch>& launches) {
+    for (const dhx_launch& l : launches) hip_check(e, launch_one(e, l), "kernel launch");
+}
+
+void set_device(dhx_engine* e) { hip_check(e, hipSetDevice(e->device), "hipSetDevice"); }
+
+double percentile_sorted(const std::vector<double>& t, int pct) {
+    // engine.rs:177-183: median = t[n/2], p95 = t[ceil(n*95/100) - 1].
+    if (pct == 50) return t[t.size() / 2];
+    return t[(t.size() * pct + 99) / 100 - 1];
+}
+
+template <class F>
+int guarded(dhx_engine* e, F&& f) {
+    try {
+        if (!e) throw dhx::Error("null engine");
+        f();
+        return 0;
+    } catch (const std::exception& ex) {
+        if (e) e->error = ex.what();
+        else dhx::set_global_error(ex.what());
+        return 1;
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+int dhx_engine_open(int32_t device, dhx_engine** out) {
+    try {
+        if (!out) throw dhx::Error("null output pointer");
+        *out = nullptr;
+        int count = 0;
+        if (hipGetDeviceCount(&count) != hipSuccess || count == 0) throw dhx::Error("no HIP device is available");
+        if (device < 0 || device >= count)
+            throw dhx::Error("device " + std::to_string(device) + " does not exist (" + std::to_string(count) +
+                             " visible)");
+        if (hipSetDevice(device) != hipSuccess) throw dhx::Error("cannot select device " + std::to_string(device));
+        hipDeviceProp_t prop;
+        if (hipGetDeviceProperties(&prop, device) != hipSuccess) throw dhx::Error("cannot query device properties");
+        const std::string arch = prop.gcnArchName;
+        if (arch.rfind("gfx950", 0) != 0)
+            throw dhx::Error("these kernels are validated for gfx950, found " + arch);
+        auto* e = new dhx_engine();
+        e->device = device;
+        if (hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess) {
+            delete e;
+            throw dhx::Error("cannot create a HIP stream");
+        }
+        *out = e;
+        return 0;
+    } catch (const std::exception& ex) {
+        dhx::set_global_error(ex.what());
+        return 1;
+    }
+}
+
+void dhx_engine_free(dhx_engine* e) {
+    if (!e) return;
+    (void)hipSetDevice(e->device);
+    if (e->stream) (void)hipStreamSynchronize(e->stream);
+    for (auto& kv : e->graphs)
+        if (kv.second.exec) (void)hipGraphExecDestroy(kv.second.exec);
+    for (void* b : e->buffers) (void)hipFree(b);
+    if (e->readback) (void)hipHostFree(e->readback);
+    if (e->stream) (void)hipStreamDestroy(e->stream);
+    delete e;
+}
+
+const char* dhx_last_error(const dhx_engine* e) { return e ? e->error.c_str() : dhx::global_error(); }
+
+int dhx_allocate(dhx_engine* e, uint64_t bytes, dhx_region* out) {
+    return guarded(e, [&] {
+        ensure_usable(e);
+        if (!out) throw dhx::Error("null output region");
+        set_device(e);
+        void* p = nullptr;
+        hip_check(e, hipMalloc(&p, std::max<uint64_t>(bytes, 16)), "hipMalloc");
+        e->buffers.push_back(p);
+        e->sizes.push_back(bytes);
+        // Zero once: padded rows of q/k/v^T are never written and must stay finite.
+        hip_check(e, hipMemset(p, 0, std::max<uint64_t>(bytes, 16)), "hipMemset");
+        *out = dhx_region{(uint32_t)(e->buffers.size() - 1), 0, bytes};
+    });
+}
+
+int dhx_weight(dhx_engine* e, const void* bytes, uint64_t n, dhx_region* out) {
+    return guarded(e, [&] {
+        if (dhx_allocate(e, n, out) != 0) throw dhx::Error(e->error);
+        hip_check(e, hipMemcpy(region_ptr(e, *out), bytes, n, hipMemcpyHostToDevice), "weight upload");
+    });
+}
+
+int dhx_upload(dhx_engine* e, dhx_region r, const void* bytes, uint64_t n) {
+    return guarded(e, [&] {
+        ensure_usable(e);
+        check_region(e, r);
+        if (n > r.bytes) throw dhx::Error("input exceeds allocated region");
+        set_device(e);
+        hip_check(e, hipMemcpyAsync(region_ptr(e, r), bytes, n, hipMemcpyHostToDevice, e->stream), "upload");
+        hip_check(e, hipStreamSynchronize(e->stream), "upload synchronize");
+    });
+}
+
+int dhx_record(dhx_engine* e, uint64_t batch, const dhx_launch* launches, uint64_t n) {
+    return guarded(e, [&] {
+        ensure_usable(e);
+        if (e->graphs.count(batch)) return;
+        std::vector<dhx_launch> list(launches, launches + n);
+        for (const dhx_launch& l : list) validate(e, l);  // before any GPU work
+        set_device(e);
+        // One linear chain on one stream: each node follows its predecessor,
+        // covering every read-before-write on reused buffers (engine.rs:110-111).
+        hip_check(e, hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal), "begin capture");
+        hipError_t launch_err = hipSuccess;
+        for (const dhx_launch& l : list) {
+            launch_err = launch_one(e, l);
+            if (launch_err != hipSuccess) break;
+        }
+        hipGraph_t graph = nullptr;
+        const hipError_t end_err = hipStreamEndCapture(e->stream, &graph);
+        if (launch_err != hipSuccess || end_err != hipSuccess) {
+            if (graph) (void)hipGraphDestroy(graph);
+            hip_check(e, launch_err != hipSuccess ? launch_err : end_err, "graph capture");
+        }
+        hipGraphExec_t exec = nullptr;
+        const hipError_t inst = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        hip_check(e, inst, "graph instantiate");
+        e->graphs[batch] = Recorded{exec, std::move(list)};
+    });
+}
+
+int dhx_has_graph(const dhx_engine* e, uint64_t batch) { return e && e->graphs.count(batch) ? 1 : 0; }
+
+int dhx_replay(dhx_engine* e, uint64_t batch) {
+    return guarded(e, [&] {
+        ensure_usable(e);
+        auto it = e->graphs.find(batch);
+        if (it == e->graphs.end()) throw dhx::Error("batch has not been prepared");
+        set_device(e);
+        hip_check(e, hipGraphLaunch(it->second.exec, e->stream), "graph launch");
+    });
+}
+
+int dhx_dispatch(dhx_engine* e, uint64_t batch) {
+    return guarded(e, [&] {
+        ensure_usable(e);
+        auto it = e->graphs.find(batch);
+        if (it == e->graphs.end()) throw dhx::Error("batch has not been prepared");
+        set_device(e);
+        run_list(e, it->second.launches);
+    });
+}
+
+int dhx_synchronize(dhx_engine* e) {
+    return guarded(e, [&] {
+        ensure_usable(e);
+        set_device(e);
+        hip_check(e, hipStreamSynchronize(e->stream), "synchronize");
+    });
+}
+
+int dhx_reserve_readback(dhx_engine* e, uint64_t bytes) {
+    return guarded(e, [&] {
+        ensure_usable(e);
+        set_device(e);
+        if (e->readback) {
+            hip_check(e, hipHostFree(e->readback), "hipHostFree");
+            e->readback = nullptr;
+            e->readback_bytes = 0;
+        }
+        hip_check(e, hipHostMalloc(&e->readback, std::max<uint64_t>(bytes, 16), hipHostMallocDefault), "hipHostMalloc");
+        e->readback_bytes = bytes;
+    });
+}
+
+int dhx_read(dhx_engine* e, dhx_region r, void* out, uint64_t n) {
+    return guarded(e, [&] {
+        ensure_usable(e);
+        if (!e->readback) throw dhx::Error("readback was not reserved");
+        if (n > e->readback_bytes) throw dhx::Error("readback exceeds reserved capacity");
+        check_region(e, r);
+        if (n > r.bytes) throw dhx::Error("output exceeds allocated region");
+        set_device(e);
+        hip_check(e, hipMemcpyAsync(e->readback, region_ptr(e, r), n, hipMemcpyDeviceToHost, e->stream), "readback copy");
+        hip_check(e, hipStreamSynchronize(e->stream), "readback synchronize");
+        std::memcpy(out, e->readback, n);
+    });
+}
+
+int dhx_benchmark(dhx_engine* e, uint64_t batch, uint64_t samples, dhx_timings* out) {
+    return guarded(e, [&] {
+        if (samples < 10) throw dhx::Error("use at least ten timing samples");
+        ensure_usable(e);
+        auto it = e->graphs.find(batch);
+        if (it == e->graphs.end()) throw dhx::Error("batch has not been prepared");
+        set_device(e);
+        std::vector<double> times[2];
+        for (uint64_t i = 0; i < samples + 10; ++i) {
+            const int order[2] = {(int)(i % 2), (int)(1 - i % 2)};
+            for (int mode : order) {
+                const auto start = std::chrono::steady_clock::now();
+                if (mode == 0) hip_check(e, hipGraphLaunch(it->second.exec, e->stream), "graph launch");
+                else run_list(e, it->second.launches);
+                hip_check(e, hipStreamSynchronize(e->stream), "synchronize");
+                const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - start).count();
+                if (i >= 10) times[mode].push_back(ms);
+            }
+        }
+        for (auto& t : times) std::sort(t.begin(), t.end());
+        out->samples = samples;
+        out->graph = dhx_distribution{percentile_sorted(times[0], 50), percentile_sorted(times[0], 95)};
+        out->direct = dhx_distribution{percentile_sorted(times[1], 50), percentile_sorted(times[1], 95)};
+    });
+}
+
+int dhx_launch_timings(dhx_engine* e, uint64_t batch, uint32_t iters, double* ms_out, uint32_t* kernel_out,
+                       uint64_t capacity, uint64_t* count) {
+    return guarded(e, [&] {
+        ensure_usable(e);
+        auto it = e->graphs.find(batch);
+        if (it == e->graphs.end()) throw dhx::Error("batch has not been prepared");
+        const auto& list = it->second.launches;
+        if (count) *count = list.size();
+        if (capacity < list.size()) throw dhx::Error("timing output too small");
+        if (iters == 0) throw dhx::Error("iters must be positive");
+        set_device(e);
+        hipEvent_t a, b;
+        hip_check(e, hipEventCreate(&a), "hipEventCreate");
+        hip_check(e, hipEventCreate(&b), "hipEventCreate");
+        for (size_t i = 0; i < list.size(); ++i) {
+            hip_check(e, launch_one(e, list[i]), "kernel launch");  // warm
+            hip_check(e, hipEventRecord(a, e->stream), "hipEventRecord");
+            for (uint32_t k = 0; k < iters; ++k) hip_check(e, launch_one(e, list[i]), "kernel launch");
+            hip_check(e, hipEventRecord(b, e->stream), "hipEventRecord");
+            hip_check(e, hipEventSynchronize(b), "hipEventSynchronize");
+            float ms = 0.f;
+            hip_check(e, hipEventElapsedTime(&ms, a, b), "hipEventElapsedTime");
+            ms_out[i] = ms / iters;
+            if (kernel_out) kernel_out[i] = list[i].kernel;
+        }
+        (void)hipEventDestroy(a);
+        (void)hipEventDestroy(b);
+    });
+}
+
+int dhx_test_fail_next_call(dhx_engine* e) {
+    return guarded(e, [&] { e->fail_next = true; });
+}
+
+}  // extern "C"

@@ -1,0 +1,159 @@
+// Online-softmax attention for gfx950 (replaces the reference's
+// kernels/attention_online_f16_wmma_cf16.loom).
+//
+// One workgroup = 4 waves = 128 queries of one (image, head); each wave owns
+// 32 queries. Keys stream through LDS in blocks of 64 (K as [key][ch], V
+// transposed as [ch][key], both double-buffered), so the same kernel serves
+// 201 tokens (224x224) and 1029 tokens (512x512).
+//
+// Everything is computed transposed so that a lane owns one query:
+//   S^T = K . Q^T      (MFMA a = K rows from LDS, b = Q^T held in registers)
+//   O^T += V^T . P^T   (MFMA a = V^T rows from LDS, b = P^T straight from the
+//                       S^T accumulators)
+// Lane l holds query (l % 32) and 16 of every 32 keys; the other 16 are in
+// lane l ^ 32, so each row max / row sum is 15 in-register ops plus one
+// cross-half exchange, and the running rescale of O^T is a per-lane scalar.
+// The score scale 1/8 is folded with log2(e) so the softmax uses v_exp_f32.
+// P is rounded to f16 for the PV product; the denominator keeps the fp32
+// weights (as in the reference, attention_online_f16_wmma_cf16.loom:195-216).
+#include "launch.hpp"
+
+namespace dhx {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int KB = 64;    // keys per LDS block
+constexpr int KLD = 72;   // LDS row pitch in halfs
+constexpr int QB = 128;   // queries per workgroup
+
+__device__ __forceinline__ half8_t zero8() {
+    half8_t z = {};
+    return z;
+}
+
+__global__ __launch_bounds__(kThreads) void attention_kernel(AttentionArgs p) {
+    __shared__ half_t sK[2][KB * KLD];
+    __shared__ half_t sV[2][kHeadDim * KLD];
+    const int qb = blockIdx.x, head = blockIdx.y, img = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l32 = lane & 31, hi = lane >> 5;
+    const int T = p.tokens;
+    const size_t bh = (size_t)img * kHeads + head;
+    const half_t* qg = p.q + bh * p.tpad * kHeadDim;
+    const half_t* kg = p.k + bh * p.tpad * kHeadDim;
+    const half_t* vg = p.vt + bh * kHeadDim * p.tpad;
+
+    const int qrow = qb * QB + wave * 32 + l32;
+    half8_t qf[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+        qf[kk] = qrow < T ? *(const half8_t*)(qg + (size_t)qrow * kHeadDim + kk * 16 + hi * 8) : zero8();
+
+    // Each thread moves two 16-byte pieces of the K block and two of V^T.
+    half8_t kr[2], vr[2];
+    auto load = [&](int kb) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int c = tid + i * kThreads, row = c >> 3, col = (c & 7) * 8;
+            kr[i] = *(const half8_t*)(kg + (size_t)(kb * KB + row) * kHeadDim + col);
+            vr[i] = *(const half8_t*)(vg + (size_t)row * p.tpad + kb * KB + col);
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int c = tid + i * kThreads, row = c >> 3, col = (c & 7) * 8;
+            *(half8_t*)(&sK[buf][row * KLD + col]) = kr[i];
+            *(half8_t*)(&sV[buf][row * KLD + col]) = vr[i];
+        }
+    };
+
+    const float scale = 0.125f * kLog2e;
+    const float neg_inf = -__builtin_inff();
+    float16_t o[2] = {float16_t{}, float16_t{}};
+    float m_run = -1e30f, l_run = 0.f;
+    const int nkb = (T + KB - 1) / KB;
+
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int kb = 0; kb < nkb; ++kb) {
+        const int buf = kb & 1;
+        const bool more = kb + 1 < nkb;
+        if (more) load(kb + 1);
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub) {
+            const int key0 = kb * KB + sub * 32;
+            if (key0 >= T) break;  // uniform across the workgroup
+            float16_t s = {};
+            const half_t* krow = &sK[buf][(sub * 32 + l32) * KLD + hi * 8];
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) s = mfma32x32x16(*(const half8_t*)(krow + kk * 16), qf[kk], s);
+            // s[r] is the score of key key0 + 8(r/4) + 4*hi + r%4 for query l32.
+            float mx = neg_inf;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = key0 + 8 * (r >> 2) + 4 * hi + (r & 3);
+                s[r] = key < T ? s[r] * scale : neg_inf;
+                mx = fmaxf(mx, s[r]);
+            }
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float m_new = fmaxf(m_run, mx);
+            const float alpha = fast_exp2(m_run - m_new);
+            float sum = 0.f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                s[r] = fast_exp2(s[r] - m_new);
+                sum += s[r];
+            }
+            sum += __shfl_xor(sum, 32, 64);
+            l_run = l_run * alpha + sum;
+            m_run = m_new;
+            o[0] *= alpha;
+            o[1] *= alpha;
+            // P^T as the b operand: k-slice element j of this lane is key
+            // key0 + 16ks + (j < 4 ? 4hi + j : 8 + 4hi + j - 4); the V^T reads
+            // below pick the same keys.
+            half8_t pb[2];
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) pb[ks][e] = (half_t)s[8 * ks + e];
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
+                    const half_t* vrow = &sV[buf][(ct * 32 + l32) * KLD + sub * 32 + ks * 16 + 4 * hi];
+                    const half4_t a0 = *(const half4_t*)vrow, a1 = *(const half4_t*)(vrow + 8);
+                    const half8_t va = __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7);
+                    o[ct] = mfma32x32x16(va, pb[ks], o[ct]);
+                }
+        }
+        if (more) store(buf ^ 1);
+        __syncthreads();
+    }
+
+    if (qrow < T) {
+        const float inv = 1.0f / l_run;
+        half_t* dst = p.out + ((size_t)img * T + qrow) * kHidden + head * kHeadDim;
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int ch = ct * 32 + g * 8 + hi * 4;
+                half4_t v = {(half_t)(o[ct][4 * g] * inv), (half_t)(o[ct][4 * g + 1] * inv),
+                             (half_t)(o[ct][4 * g + 2] * inv), (half_t)(o[ct][4 * g + 3] * inv)};
+                *(half4_t*)(dst + ch) = v;
+            }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_attention(const AttentionArgs& a, hipStream_t s) {
+    const dim3 grid((a.tokens + QB - 1) / QB, kHeads, a.images);
+    hipLaunchKernelGGL(attention_kernel, grid, dim3(kThreads), 0, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace dhx

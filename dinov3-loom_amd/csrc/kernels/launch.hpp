@@ -1,0 +1,114 @@
+// Host-side launchers for the forward-pass kernels. Each launcher assumes the
+// engine has already checked every binding's size against the shapes below
+// (engine.cpp: required_bytes); they only derive grids and launch.
+#pragma once
+#include <hip/hip_runtime.h>
+#include "common.hpp"
+
+namespace dhx {
+
+// Row LayerNorm over 384 channels, eps 1e-5, fp32 statistics.
+// x [rows][384] f16 -> out [rows][384] f16 (or f32 when f32_out).
+struct LayerNormArgs {
+    const half_t* x;
+    const float* gamma;
+    const float* beta;
+    void* out;
+    int rows;
+    int f32_out;
+};
+
+// Fused patch embedding: im2col of NCHW f32 pixels (patch order (gy, gx),
+// k order (c, dy, dx)), GEMM with patch_w [384][768] f16, + bias, narrowed to
+// f16 and scattered into x [images*T][384] after the CLS + 4 register rows,
+// which are copied from prefix [5][384] f32.
+struct PatchEmbedArgs {
+    const float* pixels;
+    const half_t* w;
+    const float* bias;
+    const float* prefix;
+    half_t* x;
+    int images;
+    int grid;  // patches per side G; image side 16*G, T = G*G + 5
+};
+
+// h [rows][384] f16 . Wqkv[1152][384]^T + b, 2D RoPE on q and k of patch
+// tokens, written head-major: q, k [images][6][tpad][64]; v transposed as
+// vt [images][6][64][tpad].
+struct QkvArgs {
+    const half_t* h;
+    const half_t* w;
+    const float* bias;
+    const float* cos;
+    const float* sin;
+    half_t* q;
+    half_t* k;
+    half_t* vt;
+    int images;
+    int grid;
+    int tpad;
+};
+
+// softmax(q k^T / 8) v per (image, head) over that image's T tokens;
+// out [images*T][384] f16 (head h in columns 64h .. 64h+63).
+struct AttentionArgs {
+    const half_t* q;
+    const half_t* k;
+    const half_t* vt;
+    half_t* out;
+    int images;
+    int tokens;
+    int tpad;
+};
+
+// x[rows][384] += ls * (a[rows][k] . W[384][k]^T + b), f16 residual in place.
+struct ResidArgs {
+    const half_t* a;
+    const half_t* w;
+    const float* bias;
+    const float* ls;
+    half_t* x;
+    int rows;
+    int k;
+};
+
+// act[rows][1536] = silu(h.Wg^T + bg) * (h.Wu^T + bu); W and b are packed
+// with gate and up rows interleaved in blocks of 32.
+struct SwigluArgs {
+    const half_t* h;
+    const half_t* w;
+    const float* bias;
+    half_t* act;
+    int rows;
+};
+
+// partials[s][rows][384] = a[:, s*k/splits ...] . W[:, s*k/splits ...]^T (f32).
+struct SplitKArgs {
+    const half_t* a;
+    const half_t* w;
+    float* partials;
+    int rows;
+    int k;
+    int splits;
+};
+
+// x[rows][384] += ls * (sum_s partials[s] + b).
+struct ReduceArgs {
+    const float* partials;
+    const float* bias;
+    const float* ls;
+    half_t* x;
+    int rows;
+    int splits;
+};
+
+hipError_t launch_layernorm(const LayerNormArgs& a, hipStream_t s);
+hipError_t launch_patch_embed(const PatchEmbedArgs& a, hipStream_t s);
+hipError_t launch_qkv_rope(const QkvArgs& a, hipStream_t s);
+hipError_t launch_attention(const AttentionArgs& a, hipStream_t s);
+hipError_t launch_resid(const ResidArgs& a, hipStream_t s);
+hipError_t launch_swiglu(const SwigluArgs& a, hipStream_t s);
+hipError_t launch_splitk(const SplitKArgs& a, hipStream_t s);
+hipError_t launch_splitk_reduce(const ReduceArgs& a, hipStream_t s);
+
+}  // namespace dhx

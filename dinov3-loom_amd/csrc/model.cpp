@@ -1,0 +1,385 @@
+// The C++ mirror of the crate's public API (src/lib.rs): DINOv3 with
+// load / from_pretrained / forward / cls / patch_mean / benchmark, batch
+// chunking, the buffer plan and the per-batch launch plan (`prepare`),
+// built on the engine C ABI exactly as lib.rs builds on HRX.
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <string>
+#include <sys/stat.h>
+#include <vector>
+
+#include "../../include/dinov3.h"
+#include "errors.hpp"
+#include "weights.hpp"
+
+namespace dhx {
+
+namespace {
+thread_local std::string g_error;
+}
+void set_global_error(const std::string& message) { g_error = message; }
+const char* global_error() { return g_error.c_str(); }
+
+namespace {
+
+constexpr uint64_t kHiddenU = 384;
+constexpr uint32_t kSplits = 4;
+
+// hub.rs:7-11
+constexpr char kRepoOwner[] = "facebook";
+constexpr char kRepoName[] = "dinov3-vits16plus-pretrain-lvd1689m";
+constexpr char kRevision[] = "c93d816fc9e567563bc068f01475bec89cc634a6";
+constexpr char kFile[] = "model.safetensors";
+
+void check_max_batch(uint64_t b) {
+    if (b < 1 || b > 64) throw Error("max_batch must be 1..=64");
+}
+
+uint32_t image_size_of(const dinov3_options& o) {
+    const uint32_t s = o.image_size == 0 ? 224 : o.image_size;
+    if (s % 16 != 0 || s < 16 || s > 1024) throw Error("image_size must be a multiple of 16 in 16..=1024");
+    return s;
+}
+
+bool exists(const std::string& p) {
+    struct stat st;
+    return ::stat(p.c_str(), &st) == 0 && S_ISREG(st.st_mode);
+}
+
+// hub.rs:17-54 with downloads unavailable: the pinned snapshot in the
+// Hugging Face cache (HF_HUB_CACHE, else HF_HOME/hub, else
+// ~/.cache/huggingface/hub), laid out as the hub client writes it.
+std::string hub_weights() {
+    std::string cache;
+    if (const char* c = std::getenv("HF_HUB_CACHE"); c && *c) cache = c;
+    else if (const char* h = std::getenv("HF_HOME"); h && *h) cache = std::string(h) + "/hub";
+    else if (const char* home = std::getenv("HOME"); home && *home) cache = std::string(home) + "/.cache/huggingface/hub";
+    else throw Error("cannot read the Hugging Face cache: no HF_HUB_CACHE, HF_HOME or HOME");
+    const std::string path = cache + "/models--" + kRepoOwner + "--" + kRepoName + "/snapshots/" + kRevision + "/" + kFile;
+    if (!exists(path))
+        throw Error(std::string(kRepoOwner) + "/" + kRepoName + " at " + kRevision + ": " + kFile +
+                    " is not cached and model downloads are disabled");
+    return path;
+}
+
+void check(int rc, dhx_engine* e) {
+    if (rc != 0) throw Error(dhx_last_error(e));
+}
+
+}  // namespace
+
+class Model {
+public:
+    Model(const std::string& path, const dinov3_options& opts) : opts_(opts) {
+        check_max_batch(opts.max_batch);
+        size_ = image_size_of(opts);
+        grid_ = size_ / 16;
+        patches_ = (uint64_t)grid_ * grid_;
+        tokens_ = patches_ + 5;
+        tpad_ = (tokens_ + 127) / 128 * 128;
+        image_elems_ = 3ull * size_ * size_;
+        // Validation and packing finish before the device is opened.
+        Packed packed = load_weights(path, grid_);
+        dhx_engine* e = nullptr;
+        if (dhx_engine_open(opts.device, &e) != 0) throw Error(dhx_last_error(nullptr));
+        engine_.reset(e);
+        for (auto& kv : packed) {
+            dhx_region r;
+            check(dhx_weight(e, kv.second.data(), kv.second.size(), &r), e);
+            weights_[kv.first] = r;
+        }
+        const uint64_t B = opts.max_batch, r = B * tokens_;
+        const uint64_t heads = B * 6 * tpad_ * 64 * 2;
+        // x, h, attn and act are f16; q/k/v^T are f16 head-major (padded rows
+        // stay zero); out, the NCHW images and the split-K slabs are f32.
+        const uint64_t sizes[kBuffers] = {r * kHiddenU * 2, r * kHiddenU * 2, heads, heads, heads, r * kHiddenU * 2,
+                                          r * 1536 * 2,     r * kHiddenU * 4, B * image_elems_ * 4,
+                                          (uint64_t)kSplits * r * kHiddenU * 4};
+        for (int i = 0; i < kBuffers; ++i) check(dhx_allocate(e, sizes[i], &a_[i]), e);
+        check(dhx_reserve_readback(e, B * tokens_ * kHiddenU * 4), e);
+    }
+
+    dhx_engine* engine() { return engine_.get(); }
+    uint64_t image_elements() const { return image_elems_; }
+    uint64_t tokens() const { return tokens_; }
+
+    void set_splitk(int mode) {
+        if (mode != 0 && mode != 1) throw Error("split-K mode must be 0 or 1");
+        splitk_ = mode;  // graphs are keyed by (batch, variant); see key()
+    }
+
+    // lib.rs:90-114
+    void forward(const float* pixels, uint64_t n, float* out, uint64_t out_floats) {
+        check_input(pixels, n);
+        const uint64_t batch = n / image_elems_;
+        const uint64_t per_image = tokens_ * kHiddenU;
+        if (out_floats < batch * per_image) throw Error("output buffer holds fewer than images*tokens*384 floats");
+        for (uint64_t first = 0; first < batch; first += opts_.max_batch) {
+            const uint64_t b = std::min<uint64_t>(opts_.max_batch, batch - first);
+            stage(pixels + first * image_elems_, b);
+            check(dhx_read(engine_.get(), region(kOut), out + first * per_image, b * per_image * 4), engine_.get());
+        }
+    }
+
+    // Upload one chunk and replay its graph (recording it on first use).
+    void stage(const float* pixels, uint64_t b) {
+        prepare(b);
+        check(dhx_upload(engine_.get(), region(kImage), pixels, b * image_elems_ * 4), engine_.get());
+        replay(b);
+    }
+
+    void replay(uint64_t b) { check(dhx_replay(engine_.get(), key(b)), engine_.get()); }
+
+    void check_input(const float* pixels, uint64_t n) const {
+        if (n % image_elems_ != 0)
+            throw Error("input must contain complete 3×" + std::to_string(size_) + "×" + std::to_string(size_) + " images");
+        for (uint64_t i = 0; i < n; ++i)
+            if (!std::isfinite(pixels[i])) throw Error("input must be finite");
+    }
+
+    // lib.rs:116-124
+    void benchmark(const float* pixels, uint64_t n, uint64_t samples, dinov3_timings* out) {
+        if (n == 0 || n > opts_.max_batch * image_elems_) throw Error("benchmark requires one nonempty batch");
+        check_input(pixels, n);
+        std::vector<float> tmp(n / image_elems_ * tokens_ * kHiddenU);
+        forward(pixels, n, tmp.data(), tmp.size());
+        check(dhx_benchmark(engine_.get(), key(n / image_elems_), samples, out), engine_.get());
+    }
+
+    // lib.rs:149-263 (prepare): one launch list per batch size, recorded as
+    // one graph; the down projection uses split-K slabs + reduce at batch 1
+    // (as the reference) or when selected, else the residual GEMM.
+    void prepare(uint64_t b) {
+        if (dhx_has_graph(engine_.get(), key(b))) return;
+        const uint32_t r = (uint32_t)(b * tokens_);
+        const uint32_t B = (uint32_t)b, G = grid_, TP = (uint32_t)tpad_;
+        std::vector<dhx_launch> l;
+        auto add = [&](uint32_t kernel, std::initializer_list<uint32_t> s, std::initializer_list<dhx_region> bind) {
+            dhx_launch x{};
+            x.kernel = kernel;
+            int i = 0;
+            for (uint32_t v : s) x.scalars[i++] = v;
+            x.n_bindings = 0;
+            for (const dhx_region& g : bind) x.bindings[x.n_bindings++] = g;
+            l.push_back(x);
+        };
+        auto w = [&](const std::string& name) { return weights_.at(name); };
+        add(DHX_K_PATCH_EMBED, {B, G}, {region(kImage), w("patch_w"), w("patch_b"), w("prefix"), region(kX)});
+        add(DHX_K_LAYERNORM, {r}, {region(kX), w("l0_norm1_w"), w("l0_norm1_b"), region(kH)});
+        const bool split = b == 1 || splitk_ == 1;
+        for (int i = 0; i < 12; ++i) {
+            const std::string p = "l" + std::to_string(i) + "_";
+            add(DHX_K_QKV_ROPE, {B, G, TP},
+                {region(kH), w(p + "qkv_w"), w(p + "qkv_b"), w("rope_cos"), w("rope_sin"), region(kQ), region(kK),
+                 region(kVt)});
+            add(DHX_K_ATTENTION, {B, G, TP}, {region(kQ), region(kK), region(kVt), region(kAttn)});
+            add(DHX_K_RESID, {r, 384}, {region(kAttn), w(p + "o_w"), w(p + "o_b"), w(p + "ls1"), region(kX)});
+            add(DHX_K_LAYERNORM, {r}, {region(kX), w(p + "norm2_w"), w(p + "norm2_b"), region(kH)});
+            add(DHX_K_SWIGLU, {r}, {region(kH), w(p + "gateup_w"), w(p + "gateup_b"), region(kAct)});
+            if (split) {
+                add(DHX_K_SPLITK, {r, 1536, kSplits}, {region(kAct), w(p + "down_w"), region(kPartials)});
+                add(DHX_K_SPLITK_REDUCE, {r, kSplits}, {region(kPartials), w(p + "down_b"), w(p + "ls2"), region(kX)});
+            } else {
+                add(DHX_K_RESID, {r, 1536}, {region(kAct), w(p + "down_w"), w(p + "down_b"), w(p + "ls2"), region(kX)});
+            }
+            if (i < 11) {
+                const std::string n = "l" + std::to_string(i + 1) + "_";
+                add(DHX_K_LAYERNORM, {r}, {region(kX), w(n + "norm1_w"), w(n + "norm1_b"), region(kH)});
+            }
+        }
+        add(DHX_K_LAYERNORM_F32, {r}, {region(kX), w("norm_w"), w("norm_b"), region(kOut)});
+        check(dhx_record(engine_.get(), key(b), l.data(), l.size()), engine_.get());
+    }
+
+    // Graph key: batch size, plus a flag bit for the split-K variant.
+    uint64_t key(uint64_t b) const { return b | (splitk_ && b > 1 ? (1ull << 32) : 0); }
+
+private:
+    enum { kX, kH, kQ, kK, kVt, kAttn, kAct, kOut, kImage, kPartials, kBuffers };
+    struct EngineFree {
+        void operator()(dhx_engine* e) const { dhx_engine_free(e); }
+    };
+    dhx_region region(int i) const { return a_[i]; }
+
+    dinov3_options opts_;
+    uint32_t size_ = 224, grid_ = 14;
+    uint64_t patches_ = 196, tokens_ = 201, tpad_ = 256, image_elems_ = 0;
+    int splitk_ = 0;
+    std::unique_ptr<dhx_engine, EngineFree> engine_;
+    std::map<std::string, dhx_region> weights_;
+    dhx_region a_[kBuffers];
+};
+
+}  // namespace dhx
+
+struct dinov3_model {
+    std::unique_ptr<dhx::Model> model;
+    std::string error;
+};
+
+namespace {
+
+template <class F>
+int guarded(dinov3_model* m, F&& f) {
+    try {
+        if (!m || !m->model) throw dhx::Error("null model");
+        f(*m->model);
+        return 0;
+    } catch (const std::exception& ex) {
+        if (m) m->error = ex.what();
+        else dhx::set_global_error(ex.what());
+        return 1;
+    }
+}
+
+template <class F>
+int guarded_global(F&& f) {
+    try {
+        f();
+        return 0;
+    } catch (const std::exception& ex) {
+        dhx::set_global_error(ex.what());
+        return 1;
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+void dinov3_options_default(dinov3_options* out) {
+    if (out) *out = dinov3_options{0, 32, 224};
+}
+
+int dinov3_load(const char* path, const dinov3_options* options, dinov3_model** out) {
+    return guarded_global([&] {
+        if (!options || !out) throw dhx::Error("null argument");
+        *out = nullptr;
+        dhx::check_max_batch(options->max_batch);  // before any file I/O
+        auto m = std::make_unique<dinov3_model>();
+        m->model = std::make_unique<dhx::Model>(path ? path : "", *options);
+        *out = m.release();
+    });
+}
+
+int dinov3_from_pretrained(const dinov3_options* options, dinov3_model** out) {
+    return guarded_global([&] {
+        if (!options || !out) throw dhx::Error("null argument");
+        *out = nullptr;
+        dhx::check_max_batch(options->max_batch);
+        const std::string path = dhx::hub_weights();
+        auto m = std::make_unique<dinov3_model>();
+        m->model = std::make_unique<dhx::Model>(path, *options);
+        *out = m.release();
+    });
+}
+
+int dinov3_hub_weights(char* path_out, uint64_t capacity) {
+    return guarded_global([&] {
+        const std::string p = dhx::hub_weights();
+        if (!path_out || capacity < p.size() + 1) throw dhx::Error("path buffer too small");
+        std::memcpy(path_out, p.c_str(), p.size() + 1);
+    });
+}
+
+int dinov3_forward(dinov3_model* m, const float* pixels, uint64_t n, float* out, uint64_t out_floats) {
+    return guarded(m, [&](dhx::Model& x) { x.forward(pixels, n, out, out_floats); });
+}
+
+int dinov3_cls(dinov3_model* m, const float* pixels, uint64_t n, float* out, uint64_t out_floats) {
+    return guarded(m, [&](dhx::Model& x) {
+        x.check_input(pixels, n);
+        const uint64_t images = n / x.image_elements(), per = x.tokens() * 384;
+        if (out_floats < images * 384) throw dhx::Error("output buffer holds fewer than images*384 floats");
+        std::vector<float> all(images * per);
+        x.forward(pixels, n, all.data(), all.size());
+        for (uint64_t i = 0; i < images; ++i) std::memcpy(out + i * 384, all.data() + i * per, 384 * sizeof(float));
+    });
+}
+
+int dinov3_patch_mean(dinov3_model* m, const float* pixels, uint64_t n, float* out, uint64_t out_floats) {
+    return guarded(m, [&](dhx::Model& x) {
+        x.check_input(pixels, n);
+        const uint64_t images = n / x.image_elements(), T = x.tokens(), per = T * 384;
+        if (out_floats < images * 384) throw dhx::Error("output buffer holds fewer than images*384 floats");
+        std::vector<float> all(images * per);
+        x.forward(pixels, n, all.data(), all.size());
+        const float patches = (float)(T - 5);
+        for (uint64_t i = 0; i < images; ++i) {
+            float* o = out + i * 384;
+            for (int c = 0; c < 384; ++c) o[c] = 0.f;
+            // lib.rs:139-144: float32 `+= v / 196` in token order.
+            for (uint64_t t = 5; t < T; ++t) {
+                const float* row = all.data() + i * per + t * 384;
+                for (int c = 0; c < 384; ++c) o[c] += row[c] / patches;
+            }
+        }
+    });
+}
+
+int dinov3_benchmark(dinov3_model* m, const float* pixels, uint64_t n, uint64_t samples, dinov3_timings* out) {
+    return guarded(m, [&](dhx::Model& x) {
+        if (!out) throw dhx::Error("null timings");
+        x.benchmark(pixels, n, samples, out);
+    });
+}
+
+const char* dinov3_last_error(const dinov3_model* m) { return m ? m->error.c_str() : dhx::global_error(); }
+
+void dinov3_free(dinov3_model* m) { delete m; }
+
+uint64_t dinov3_image_elements(const dinov3_model* m) { return m && m->model ? m->model->image_elements() : 0; }
+
+uint64_t dinov3_tokens(const dinov3_model* m) { return m && m->model ? m->model->tokens() : 0; }
+
+dhx_engine* dinov3_engine(dinov3_model* m) { return m && m->model ? m->model->engine() : nullptr; }
+
+int dinov3_stage(dinov3_model* m, const float* pixels, uint64_t n) {
+    return guarded(m, [&](dhx::Model& x) {
+        x.check_input(pixels, n);
+        const uint64_t b = n / x.image_elements();
+        if (b == 0) throw dhx::Error("stage requires one nonempty batch");
+        x.stage(pixels, b);
+    });
+}
+
+int dinov3_replay(dinov3_model* m, uint64_t images) {
+    return guarded(m, [&](dhx::Model& x) { x.replay(images); });
+}
+
+int dinov3_set_splitk(dinov3_model* m, int mode) {
+    return guarded(m, [&](dhx::Model& x) { x.set_splitk(mode); });
+}
+
+int dinov3_write_random_weights(const char* path, uint64_t seed, int preset) {
+    return guarded_global([&] {
+        if (!path) throw dhx::Error("null path");
+        dhx::write_random_weights(path, seed, preset);
+    });
+}
+
+int dinov3_random_pixels(uint64_t seed, uint64_t images, uint32_t image_size, float* out) {
+    return guarded_global([&] {
+        if (image_size == 0 || !out) throw dhx::Error("bad arguments");
+        dhx::random_pixels(seed, images, image_size, out);
+    });
+}
+
+int dinov3_patchify(const float* pixels, uint64_t images, uint32_t image_size, float* out) {
+    return guarded_global([&] {
+        if (image_size % 16 != 0 || image_size == 0) throw dhx::Error("image_size must be a multiple of 16");
+        dhx::patchify(pixels, images, image_size, out);
+    });
+}
+
+int dinov3_pack_f16(const char* name, const float* values, uint64_t n, uint16_t* out) {
+    return guarded_global([&] {
+        const std::vector<uint8_t> b = dhx::pack_f16(name ? name : "", values, n);
+        std::memcpy(out, b.data(), b.size());
+    });
+}
+
+}  // extern "C"

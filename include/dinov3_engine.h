@@ -1,0 +1,132 @@
+/*
+ * dinov3_engine.h -- engine-level C ABI: the thin FFI layer a Rust
+ * `src/engine.rs` binds in place of the HRX runtime surface it uses today
+ * (hrx::{Device, Stream, Buffer, GraphExec, Kernel, Constants} and
+ * hrx::loom::{Compiler, Kernels}; engine.rs:1-3). One engine = one device,
+ * one HIP stream, resident buffers, one instantiated hipGraph per batch size.
+ *
+ * Conventions: every function returns 0 on success and nonzero on failure;
+ * the message is then available from dhx_last_error(engine) (or
+ * dhx_last_error(NULL) when no engine exists yet). After any failed HIP call
+ * the engine is poisoned and later calls fail with "session is unusable
+ * after a GPU failure" (engine.rs:36, 93, 168-171, 192-201, 204-213).
+ * An engine is not thread-safe; separate engines are independent.
+ */
+#ifndef DINOV3_ENGINE_H
+#define DINOV3_ENGINE_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct dhx_engine dhx_engine;
+
+/* A byte range of one engine buffer; replaces engine.rs:6-20 `Region`. */
+typedef struct dhx_region {
+    uint32_t buffer;
+    uint64_t offset;
+    uint64_t bytes;
+} dhx_region;
+
+/* Kernel table; replaces the `specifications()` list (lib.rs:281-300).
+ * Scalars and bindings (in order) per kernel:
+ *   DHX_K_PATCH_EMBED   s = {images, grid}           b = {pixels f32 NCHW, patch_w f16 [384][768],
+ *                                                          patch_b f32 [384], prefix f32 [5][384], x f16}
+ *   DHX_K_LAYERNORM     s = {rows}                   b = {x f16, gamma f32, beta f32, out f16}
+ *   DHX_K_LAYERNORM_F32 s = {rows}                   b = {x f16, gamma f32, beta f32, out f32}
+ *   DHX_K_QKV_ROPE      s = {images, grid, tpad}     b = {h f16, qkv_w f16 [1152][384], qkv_b f32,
+ *                                                          rope_cos f32 [P][64], rope_sin f32, q, k, vt}
+ *   DHX_K_ATTENTION     s = {images, grid, tpad}     b = {q, k, vt, out f16 [rows][384]}
+ *   DHX_K_RESID         s = {rows, k}                b = {a f16 [rows][k], w f16 [384][k], b f32, ls f32, x f16}
+ *   DHX_K_SWIGLU        s = {rows}                   b = {h f16, gateup_w f16 [3072][384], gateup_b f32, act f16}
+ *   DHX_K_SPLITK        s = {rows, k, splits}        b = {a f16, w f16 [384][k], partials f32 [splits][rows][384]}
+ *   DHX_K_SPLITK_REDUCE s = {rows, splits}           b = {partials f32, b f32, ls f32, x f16}
+ * q and k are [images][6][tpad][64] f16, vt is [images][6][64][tpad] f16,
+ * tpad a multiple of 128 >= T = grid*grid + 5. Every binding's size is
+ * checked against these shapes before anything is launched or recorded. */
+enum {
+    DHX_K_PATCH_EMBED = 0,
+    DHX_K_LAYERNORM = 1,
+    DHX_K_LAYERNORM_F32 = 2,
+    DHX_K_QKV_ROPE = 3,
+    DHX_K_ATTENTION = 4,
+    DHX_K_RESID = 5,
+    DHX_K_SWIGLU = 6,
+    DHX_K_SPLITK = 7,
+    DHX_K_SPLITK_REDUCE = 8,
+    DHX_KERNEL_COUNT = 9
+};
+
+#define DHX_MAX_SCALARS 4
+#define DHX_MAX_BINDINGS 8
+
+/* One dispatch; replaces engine.rs:21-27 `Launch`. The grid is derived from
+ * the scalars by each kernel's launcher. */
+typedef struct dhx_launch {
+    uint32_t kernel;
+    uint32_t scalars[DHX_MAX_SCALARS];
+    uint32_t n_bindings;
+    dhx_region bindings[DHX_MAX_BINDINGS];
+} dhx_launch;
+
+/* Host-clock milliseconds around submission and completion; replaces
+ * engine.rs:272-284 `ForwardTimings` / `Distribution`. */
+typedef struct dhx_distribution {
+    double median_ms;
+    double p95_ms;
+} dhx_distribution;
+
+typedef struct dhx_timings {
+    uint64_t samples;
+    dhx_distribution graph;
+    dhx_distribution direct;
+} dhx_timings;
+
+/* engine.rs:40-59 (Engine::new): open the device and create the stream.
+ * Fails unless the device is gfx950. */
+int dhx_engine_open(int32_t device, dhx_engine **out);
+void dhx_engine_free(dhx_engine *e);
+const char *dhx_last_error(const dhx_engine *e);
+
+/* engine.rs:60-64 (allocate): zero-initialised device buffer. */
+int dhx_allocate(dhx_engine *e, uint64_t bytes, dhx_region *out);
+/* engine.rs:65-70 (weight): allocate and upload. */
+int dhx_weight(dhx_engine *e, const void *bytes, uint64_t n, dhx_region *out);
+/* engine.rs:191-202 (upload). */
+int dhx_upload(dhx_engine *e, dhx_region r, const void *bytes, uint64_t n);
+/* engine.rs:87-129 (record): validate the launch list, capture it as one
+ * hipGraph for `batch` and keep it with its launch list. Recording a batch
+ * that already has a graph is a no-op. */
+int dhx_record(dhx_engine *e, uint64_t batch, const dhx_launch *launches, uint64_t n);
+int dhx_has_graph(const dhx_engine *e, uint64_t batch);
+/* engine.rs:203-214 (replay): launch the graph recorded for `batch`. */
+int dhx_replay(dhx_engine *e, uint64_t batch);
+/* Direct dispatch of the launch list recorded for `batch` (the "direct"
+ * mode of engine.rs:140-163). */
+int dhx_dispatch(dhx_engine *e, uint64_t batch);
+int dhx_synchronize(dhx_engine *e);
+/* engine.rs:215-218 (reserve_readback): pinned host staging buffer. */
+int dhx_reserve_readback(dhx_engine *e, uint64_t bytes);
+/* engine.rs:219-269 (read): device -> pinned staging -> caller memory. */
+int dhx_read(dhx_engine *e, dhx_region r, void *out, uint64_t n);
+/* engine.rs:130-190 (benchmark): samples >= 10; samples + 10 iterations of
+ * graph replay and direct dispatch in alternating order, first 10 dropped. */
+int dhx_benchmark(dhx_engine *e, uint64_t batch, uint64_t samples, dhx_timings *out);
+
+/* No reference counterpart (measurement hook): average device time of each
+ * launch of `batch`'s list, from HIP events on the engine's stream over
+ * `iters` direct dispatches of that launch alone. ms_out has one slot per
+ * launch; kernel_out (optional) receives each launch's kernel id. */
+int dhx_launch_timings(dhx_engine *e, uint64_t batch, uint32_t iters, double *ms_out,
+                       uint32_t *kernel_out, uint64_t capacity, uint64_t *count);
+
+/* No reference counterpart (test hook): make the next HIP-facing engine call
+ * fail as if the runtime had returned an error, to exercise poisoning. */
+int dhx_test_fail_next_call(dhx_engine *e);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

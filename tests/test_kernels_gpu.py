@@ -1,0 +1,255 @@
+"""Per-kernel parity on the GPU: each HIP kernel is launched alone through the
+engine C ABI (record + graph replay) on seeded inputs and compared with the
+float64 oracle's per-op functions applied to the same float16 inputs.
+
+Tolerances (float16 outputs, fp32 accumulation): |gpu - ref| <= 2^-10 |ref|
++ atol, i.e. one float16 ulp of the result plus an absolute floor stated per
+test; cosine > 0.99999. Attention rounds P to float16 before PV (as the
+reference does), so its floor is 2^-9 max|V|."""
+import os
+
+import numpy as np
+import pytest
+
+import dinov3_hrx as d
+import oracle
+
+from conftest import cosine
+
+pytestmark = pytest.mark.gpu
+
+K_PATCH, K_LN, K_LN32, K_QKV, K_ATTN, K_RESID, K_SWIGLU, K_SPLITK, K_REDUCE = range(9)
+_keys = iter(range(1000, 100000))
+
+
+@pytest.fixture(scope="module")
+def eng(gpu):
+    oracle.set_threads(min(16, os.cpu_count() or 1))
+    e = d.Engine(0)
+    e.reserve_readback(512 << 20)
+    yield e
+    e.close()
+
+
+def up(e, arr):
+    a = np.ascontiguousarray(arr)
+    r = e.allocate(a.nbytes)
+    e.upload(r, a)
+    return r
+
+
+def run(e, kernel, scalars, bindings):
+    key = next(_keys)
+    e.record(key, [(kernel, scalars, bindings)])
+    e.replay(key)
+    e.synchronize()
+
+
+def f16(a):
+    return np.asarray(a, np.float16)
+
+
+def check(gpu, ref, atol, rel=2.0**-10, cos_min=0.99999, what=""):
+    g = np.asarray(gpu, np.float64)
+    r = np.asarray(ref, np.float64)
+    assert g.shape == r.shape, (g.shape, r.shape)
+    assert np.all(np.isfinite(g)), what
+    err = np.abs(g - r)
+    bound = rel * np.abs(r) + atol
+    worst = np.unravel_index(np.argmax(err - bound), err.shape)
+    assert np.all(err <= bound), f"{what}: max err {err.max():.3g}, worst at {worst}: gpu {g[worst]} ref {r[worst]}"
+    c = cosine(g, r)
+    assert c > cos_min, f"{what}: cosine {c}"
+    print(f"{what}: max_abs {err.max():.3g} cos {c:.9f}")
+    return err.max()
+
+
+@pytest.mark.parametrize("rows", [1, 1001, 12864])
+@pytest.mark.parametrize("f32_out", [False, True])
+def test_layernorm(eng, rows, f32_out):
+    rng = np.random.default_rng(rows)
+    x = f16(rng.normal(size=(rows, 384)) * 2 + 0.5)
+    x[0] = 1.5  # a constant row normalises to beta
+    g = rng.normal(size=384).astype(np.float32)
+    b = rng.normal(size=384).astype(np.float32)
+    out = eng.allocate(rows * 384 * (4 if f32_out else 2))
+    run(eng, K_LN32 if f32_out else K_LN, [rows], [up(eng, x), up(eng, g), up(eng, b), out])
+    y = eng.read(out, np.float32 if f32_out else np.float16, (rows, 384))
+    ref = oracle.layernorm(x.astype(np.float64), g, b)
+    check(y, ref, atol=1e-4 if not f32_out else 2e-5, rel=2.0**-10 if not f32_out else 1e-5, what=f"LN rows={rows}")
+
+
+def patch_case(eng, images, grid, px, w, b, prefix):
+    T = grid * grid + 5
+    x = eng.allocate(images * T * 384 * 2)
+    run(eng, K_PATCH, [images, grid], [up(eng, px), up(eng, w), up(eng, b), up(eng, prefix), x])
+    return eng.read(x, np.float16, (images, T, 384))
+
+
+@pytest.mark.parametrize("images,grid", [(3, 14), (1, 32), (5, 4)])
+def test_patch_embed(eng, images, grid):
+    rng = np.random.default_rng(images * 100 + grid)
+    S = 16 * grid
+    px = rng.normal(size=(images, 3, S, S)).astype(np.float32)
+    w = f16(rng.normal(size=(384, 768)) * 0.02)
+    b = rng.normal(size=384).astype(np.float32) * 0.1
+    prefix = rng.normal(size=(5, 384)).astype(np.float32)
+    y = patch_case(eng, images, grid, px, w, b, prefix)
+    a = oracle.round_f16(oracle.patchify(px, grid))  # the kernel narrows pixels to f16 while staging
+    ref = oracle.linear(a, w.astype(np.float64), b).reshape(images, grid * grid, 384)
+    check(y[:, 5:], ref, atol=2e-4, what=f"patch embed {images}x{grid}")
+    assert np.array_equal(y[:, :5], np.broadcast_to(f16(prefix), (images, 5, 384)))
+
+
+def test_patch_embed_permutation_kat(eng):
+    # lib.rs:307-327 on the GPU: with one-hot weights the output columns are
+    # pixels, so the im2col gather must reproduce patchify's order exactly.
+    images, grid = 2, 14
+    px = (np.arange(images * 3 * 224 * 224) % 2039).astype(np.float32).reshape(images, 3, 224, 224)
+    want_all = oracle.patchify(px, grid).reshape(images, 196, 768)
+    for parity in (0, 1):
+        cols = 2 * np.arange(384) + parity
+        w = np.zeros((384, 768), np.float16)
+        w[np.arange(384), cols] = 1
+        y = patch_case(eng, images, grid, px, w, np.zeros(384, np.float32), np.zeros((5, 384), np.float32))
+        assert np.array_equal(y[:, 5:].astype(np.float32), want_all[:, :, cols])
+
+
+def head_major(x, images, T, tpad):
+    """[images*T, 384] -> [images, 6, tpad, 64] with zero padding."""
+    out = np.zeros((images, 6, tpad, 64), x.dtype)
+    out[:, :, :T] = x.reshape(images, T, 6, 64).transpose(0, 2, 1, 3)
+    return out
+
+
+@pytest.mark.parametrize("images,grid", [(3, 14), (1, 32), (2, 4)])
+def test_qkv_rope(eng, images, grid):
+    rng = np.random.default_rng(7 + grid)
+    T = grid * grid + 5
+    tpad = (T + 127) // 128 * 128
+    h = f16(rng.normal(size=(images * T, 384)))
+    w = f16(rng.normal(size=(1152, 384)) * 0.05)
+    b = (rng.normal(size=1152) * 0.1).astype(np.float32)
+    cos, sin = oracle.rope_tables(grid)
+    nb = images * 6 * tpad * 64 * 2
+    q, k, vt = eng.allocate(nb), eng.allocate(nb), eng.allocate(nb)
+    run(eng, K_QKV, [images, grid, tpad], [up(eng, h), up(eng, w), up(eng, b), up(eng, cos), up(eng, sin), q, k, vt])
+    gq = eng.read(q, np.float16, (images, 6, tpad, 64))
+    gk = eng.read(k, np.float16, (images, 6, tpad, 64))
+    gv = eng.read(vt, np.float16, (images, 6, 64, tpad))
+    hd = h.astype(np.float64)
+    for i in range(images):
+        rows = hd[i * T:(i + 1) * T]
+        rq = oracle.rope(oracle.linear(rows, w[:384].astype(np.float64), b[:384]), grid)
+        rk = oracle.rope(oracle.linear(rows, w[384:768].astype(np.float64), b[384:768]), grid)
+        rv = oracle.linear(rows, w[768:].astype(np.float64), b[768:])
+        to_tok = lambda a: a.transpose(1, 0, 2).reshape(T, 384)
+        check(to_tok(gq[i, :, :T]), rq, atol=1e-3, what=f"q img {i}")
+        check(to_tok(gk[i, :, :T]), rk, atol=1e-3, what=f"k img {i}")
+        check(gv[i, :, :, :T].transpose(2, 0, 1).reshape(T, 384), rv, atol=1e-3, what=f"v img {i}")
+    # padded rows / columns are never written
+    assert not gq[:, :, T:].any() and not gk[:, :, T:].any() and not gv[:, :, :, T:].any()
+
+
+@pytest.mark.parametrize("images,grid,qscale", [(2, 14, 2.0), (1, 32, 2.0), (3, 4, 4.0), (1, 14, 0.0)])
+def test_attention(eng, images, grid, qscale):
+    rng = np.random.default_rng(int(grid * 10 + qscale))
+    T = grid * grid + 5
+    tpad = (T + 127) // 128 * 128
+    q = f16(rng.normal(size=(images * T, 384)) * qscale)
+    k = f16(rng.normal(size=(images * T, 384)))
+    v = f16(rng.normal(size=(images * T, 384)))
+    vt = head_major(v, images, T, tpad).transpose(0, 1, 3, 2).copy()
+    out = eng.allocate(images * T * 384 * 2)
+    run(eng, K_ATTN, [images, grid, tpad],
+        [up(eng, head_major(q, images, T, tpad)), up(eng, head_major(k, images, T, tpad)), up(eng, vt), out])
+    y = eng.read(out, np.float16, (images * T, 384))
+    for i in range(images):
+        sl = slice(i * T, (i + 1) * T)
+        ref = oracle.attention(q[sl].astype(np.float64), k[sl].astype(np.float64), v[sl].astype(np.float64))
+        check(y[sl], ref, atol=2.0**-9 * np.abs(v[sl]).max(), cos_min=0.9999, what=f"attention T={T} img {i}")
+
+
+@pytest.mark.parametrize("rows,kdim", [(1001, 384), (1001, 1536), (201, 1536), (12864, 384)])
+def test_resid(eng, rows, kdim):
+    rng = np.random.default_rng(rows + kdim)
+    a = f16(rng.normal(size=(rows, kdim)))
+    w = f16(rng.normal(size=(384, kdim)) * 0.03)
+    b = (rng.normal(size=384) * 0.1).astype(np.float32)
+    ls = rng.uniform(0.5, 1.5, size=384).astype(np.float32)
+    x0 = f16(rng.normal(size=(rows, 384)))
+    x = up(eng, x0)
+    run(eng, K_RESID, [rows, kdim], [up(eng, a), up(eng, w), up(eng, b), up(eng, ls), x])
+    y = eng.read(x, np.float16, (rows, 384))
+    ref = x0.astype(np.float64) + ls * oracle.linear(a.astype(np.float64), w.astype(np.float64), b)
+    check(y, ref, atol=2e-3, what=f"resid rows={rows} k={kdim}")
+
+
+def pack_gateup(wg, wu, bg, bu):
+    """The loader's layout: blocks of 32 gate rows then the 32 matching up rows."""
+    w = np.empty((3072, 384), wg.dtype)
+    b = np.empty(3072, np.float32)
+    for blk in range(48):
+        w[64 * blk:64 * blk + 32] = wg[32 * blk:32 * blk + 32]
+        w[64 * blk + 32:64 * blk + 64] = wu[32 * blk:32 * blk + 32]
+        b[64 * blk:64 * blk + 32] = bg[32 * blk:32 * blk + 32]
+        b[64 * blk + 32:64 * blk + 64] = bu[32 * blk:32 * blk + 32]
+    return w, b
+
+
+@pytest.mark.parametrize("rows", [1001, 12864])
+def test_swiglu(eng, rows):
+    rng = np.random.default_rng(rows)
+    h = f16(rng.normal(size=(rows, 384)))
+    wg, wu = f16(rng.normal(size=(1536, 384)) * 0.05), f16(rng.normal(size=(1536, 384)) * 0.05)
+    bg, bu = (rng.normal(size=1536) * 0.2).astype(np.float32), (rng.normal(size=1536) * 0.2).astype(np.float32)
+    w, b = pack_gateup(wg, wu, bg, bu)
+    act = eng.allocate(rows * 1536 * 2)
+    run(eng, K_SWIGLU, [rows], [up(eng, h), up(eng, w), up(eng, b), act])
+    y = eng.read(act, np.float16, (rows, 1536))
+    hd = h.astype(np.float64)
+    ref = oracle.swiglu(oracle.linear(hd, wg.astype(np.float64), bg), oracle.linear(hd, wu.astype(np.float64), bu))
+    check(y, ref, atol=2e-3, what=f"swiglu rows={rows}")
+
+
+@pytest.mark.parametrize("rows", [201, 1001])
+def test_splitk_and_reduce(eng, rows):
+    rng = np.random.default_rng(rows + 5)
+    kdim, splits = 1536, 4
+    a = f16(rng.normal(size=(rows, kdim)))
+    w = f16(rng.normal(size=(384, kdim)) * 0.03)
+    b = (rng.normal(size=384) * 0.1).astype(np.float32)
+    ls = rng.uniform(0.5, 1.5, size=384).astype(np.float32)
+    x0 = f16(rng.normal(size=(rows, 384)))
+    part = eng.allocate(splits * rows * 384 * 4)
+    run(eng, K_SPLITK, [rows, kdim, splits], [up(eng, a), up(eng, w), part])
+    p = eng.read(part, np.float32, (splits, rows, 384))
+    ad, wd = a.astype(np.float64), w.astype(np.float64)
+    c = kdim // splits
+    for s in range(splits):
+        ref = oracle.linear(ad[:, s * c:(s + 1) * c], wd[:, s * c:(s + 1) * c])
+        check(p[s], ref, atol=1e-4, rel=1e-5, what=f"split {s}")
+    x = up(eng, x0)
+    run(eng, K_REDUCE, [rows, splits], [part, up(eng, b), up(eng, ls), x])
+    y = eng.read(x, np.float16, (rows, 384))
+    ref = x0.astype(np.float64) + ls * oracle.linear(ad, wd, b)
+    check(y, ref, atol=2e-3, what="split-K reduce")
+
+
+def test_launch_validation_happens_before_any_launch(eng):
+    small = eng.allocate(64)
+    g = up(eng, np.ones(384, np.float32))
+    with pytest.raises(d.DINOv3Error, match="needs"):
+        eng.record(next(_keys), [(K_LN, [10], [small, g, g, small])])
+    big = eng.allocate(10 * 384 * 2 + 64)
+    mis = d.region_slice(big, 8, 10 * 384 * 2)
+    with pytest.raises(d.DINOv3Error, match="aligned"):
+        eng.record(next(_keys), [(K_LN, [10], [mis, g, g, big])])
+    with pytest.raises(d.DINOv3Error, match="unknown kernel"):
+        eng.record(next(_keys), [(42, [1], [big])])
+    with pytest.raises(d.DINOv3Error, match="takes 4 bindings"):
+        eng.record(next(_keys), [(K_LN, [10], [big, g])])
+    with pytest.raises(d.DINOv3Error, match="tpad"):
+        eng.record(next(_keys), [(K_ATTN, [1, 14, 200], [big, big, big, big])])
+    with pytest.raises(d.DINOv3Error, match="not been prepared"):
+        eng.replay(987654321)

@@ -1,0 +1,166 @@
+"""Whole-forward parity and API behaviour on the GPU (tests/model.rs:61-99
+restated on seeded random-init weights, plus the configs of BASELINE.json).
+
+Parity bar: all-token and CLS cosine against the float64 oracle > 0.9999
+(tests/model.rs:85-86), max-abs error printed; batched vs single-image
+cosine > 0.99999 (tests/model.rs:87-93); bitwise determinism of a repeated
+batched forward (tests/model.rs:95)."""
+import os
+
+import numpy as np
+import pytest
+
+import dinov3_hrx as d
+import oracle
+
+from conftest import cosine
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _threads(gpu):
+    oracle.set_threads(min(16, os.cpu_count() or 1))
+
+
+@pytest.fixture(scope="module")
+def models(weight_file):
+    cache = {}
+
+    def get(preset=0, max_batch=4, image_size=224):
+        key = (preset, max_batch, image_size)
+        if key not in cache:
+            cache[key] = d.DINOv3.load(weight_file(preset), d.Options(0, max_batch, image_size))
+        return cache[key]
+
+    yield get
+    for m in cache.values():
+        m.close()
+
+
+def compare(got, want, what):
+    got = np.asarray(got, np.float64)
+    err = np.abs(got - want).max()
+    c_all, c_cls = cosine(got, want), cosine(got[0], want[0])
+    print(f"{what}: all-token cos {c_all:.7f}  CLS cos {c_cls:.7f}  max-abs {err:.4g}")
+    return c_all, c_cls, err
+
+
+@pytest.mark.parametrize("preset", [0, 1])
+def test_forward_matches_oracle(models, oracle_weights, preset):
+    m = models(preset)
+    px = d.random_pixels(1, 2)
+    out = m.forward(px)
+    assert out.shape == (2, 201, 384) and out.dtype == np.float32
+    for i in range(2):
+        want = oracle.forward(oracle_weights(preset), px[i], 14)
+        c_all, c_cls, _ = compare(out[i], want, f"preset {preset} image {i}")
+        assert c_all > 0.9999 and c_cls > 0.9999
+
+
+def test_acceptance_pattern_and_changing_batch(models, oracle_weights):
+    # tests/model.rs:61-99 with its input sin(0.037 i) * 0.6 over 4 images.
+    m = models(1)
+    images = (np.sin(np.arange(4 * d.IMAGE_ELEMENTS, dtype=np.float64) * 0.037) * 0.6).astype(np.float32)
+    batched = m.forward(images)
+    for i in range(4):
+        img = images[i * d.IMAGE_ELEMENTS:(i + 1) * d.IMAGE_ELEMENTS]
+        got = m.forward(img)[0]
+        want = oracle.forward(oracle_weights(1), img, 14)
+        c_all, c_cls, _ = compare(got, want, f"acceptance image {i}")
+        assert c_all > 0.9999 and c_cls > 0.9999
+        assert cosine(batched[i], got) > 0.99999
+    assert np.array_equal(m.forward(images), batched)  # bitwise determinism
+    with pytest.raises(d.DINOv3Error, match="complete 3×224×224 images"):
+        m.forward(np.zeros(3, np.float32))
+    with pytest.raises(d.DINOv3Error, match="finite"):
+        m.forward(np.full(d.IMAGE_ELEMENTS, np.nan, np.float32))
+
+
+def test_chunking_and_empty(models):
+    m = models(1, max_batch=4)
+    px = d.random_pixels(3, 10)
+    out = m.forward(px)
+    assert out.shape == (10, 201, 384)
+    # chunks are [0..4), [4..8), [8..10); the last chunk equals a batch of 2
+    assert np.array_equal(out[8:], m.forward(px[8:]))
+    assert np.array_equal(out[4:8], m.forward(px[4:8]))
+    assert m.forward(np.zeros(0, np.float32)).shape == (0, 201, 384)
+
+
+def test_cls_and_patch_mean(models):
+    m = models(1)
+    px = d.random_pixels(4, 3)
+    out = m.forward(px)
+    assert np.array_equal(m.cls(px), out[:, 0])
+    pm = m.patch_mean(px)
+    want = np.zeros((3, 384), np.float32)
+    for t in range(5, 201):  # lib.rs:139-144: float32 += v / 196 in token order
+        want += out[:, t] / np.float32(196)
+    assert np.array_equal(pm, want)
+
+
+def test_full_batch_64_rows_independent_of_batch(models, oracle_weights):
+    # Config 3 (b = 64, 12,864 token rows): every row's arithmetic is the same
+    # whatever the batch, so the first and last images of the b = 64 forward
+    # equal bitwise the same images run as a batch of 2.
+    m = models(0, max_batch=64)
+    px = d.random_pixels(1, 64)
+    out = m.forward(px)
+    assert np.all(np.isfinite(out))
+    assert np.array_equal(out[:2], m.forward(px[:2]))
+    assert np.array_equal(out[62:], m.forward(px[62:]))
+    for i in (0, 63):
+        c_all, c_cls, _ = compare(out[i], oracle.forward(oracle_weights(0), px[i], 14), f"b64 image {i}")
+        assert c_all > 0.9999 and c_cls > 0.9999
+
+
+def test_splitk_variant(models):
+    m = models(1, max_batch=8)
+    px = d.random_pixels(5, 8)
+    base = m.forward(px)
+    m.set_splitk(1)
+    try:
+        split = m.forward(px)
+    finally:
+        m.set_splitk(0)
+    for i in range(8):
+        assert cosine(split[i], base[i]) > 0.99999
+    assert np.array_equal(m.forward(px), base)
+
+
+@pytest.mark.parametrize("preset", [0, 1])
+def test_512_high_resolution(models, oracle_weights, preset):
+    # Config 5: 512x512, 1024 patches + 5 = 1029 tokens, RoPE on the 32x32 grid.
+    m = models(preset, max_batch=2, image_size=512)
+    assert m.tokens == 1029
+    px = d.random_pixels(1, 1, 512)
+    out = m.forward(px)
+    assert out.shape == (1, 1029, 384)
+    c_all, c_cls, _ = compare(out[0], oracle.forward(oracle_weights(preset), px[0], 32), f"512 preset {preset}")
+    assert c_all > 0.9999 and c_cls > 0.9999
+
+
+def test_benchmark(models):
+    m = models(0)
+    px = d.random_pixels(1, 4)
+    t = m.benchmark(px, 10)
+    assert t.samples == 10 and 0 < t.graph.median_ms <= t.graph.p95_ms and 0 < t.direct.median_ms
+    with pytest.raises(d.DINOv3Error, match="at least ten"):
+        m.benchmark(px, 9)
+    with pytest.raises(d.DINOv3Error, match="one nonempty batch"):
+        m.benchmark(d.random_pixels(1, 5), 10)
+    with pytest.raises(d.DINOv3Error, match="one nonempty batch"):
+        m.benchmark(np.zeros(0, np.float32), 10)
+
+
+def test_gpu_failure_poisons_session(weight_file):
+    m = d.DINOv3.load(weight_file(0), d.Options(0, 2))
+    px = d.random_pixels(1, 1)
+    m.forward(px)
+    m._fail_next_gpu_call()
+    with pytest.raises(d.DINOv3Error):
+        m.forward(px)
+    with pytest.raises(d.DINOv3Error, match="session is unusable after a GPU failure"):
+        m.forward(px)
+    m.close()
