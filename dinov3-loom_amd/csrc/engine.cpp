@@ -113,7 +113,7 @@ Need required(const dhx_launch& l) {
         }
         case DHX_K_RESID: {
             positive(s[0], "rows");
-            if (s[1] == 0 || s[1] % 64 != 0) throw dhx::Error("k must be a positive multiple of 64");
+            if (s[1] == 0 || s[1] % 128 != 0) throw dhx::Error("k must be a positive multiple of 128");
             return {5, {s[0] * (uint64_t)s[1] * 2, H * s[1] * 2, H * 4, H * 4, s[0] * H * 2}};
         }
         case DHX_K_SWIGLU:
@@ -122,7 +122,7 @@ Need required(const dhx_launch& l) {
         case DHX_K_SPLITK: {
             positive(s[0], "rows");
             positive(s[2], "splits");
-            if (s[1] == 0 || s[1] % (64ull * s[2]) != 0) throw dhx::Error("k must split into multiples of 64");
+            if (s[1] == 0 || s[1] % (128ull * s[2]) != 0) throw dhx::Error("k must split into multiples of 128");
             return {3, {s[0] * (uint64_t)s[1] * 2, H * s[1] * 2, (uint64_t)s[2] * s[0] * H * 4}};
         }
         case DHX_K_SPLITK_REDUCE:

@@ -1,0 +1,245 @@
+// f16 MFMA GEMM core for gfx950: C[m][n] = sum_k A[m][k] * W[n][k], fp32
+// accumulation, shared by every GEMM variant of the forward pass.
+//
+// A workgroup of WGM x WGN waves owns a BM x BN output tile; the K loop walks
+// 64-wide stages. Stages move HBM/L2 -> registers -> LDS with two register
+// sets and two LDS buffers, so the global loads of stage s+2 are in flight
+// while stage s feeds the MFMAs and stage s+1 is written to LDS. The LDS
+// barrier only waits for LDS traffic (s_waitcnt lgkmcnt(0); s_barrier):
+// __syncthreads() would also drain every outstanding global load (its
+// workgroup release fence waits on vmcnt(0)) and serialise the pipeline.
+// Prefetch loads are unconditional (the stage index is clamped at the end)
+// so the compiler's vmcnt waits count exactly the loads they need.
+//
+// Each wave owns TM x TN of the tile as 32x32 tiles of
+// v_mfma_f32_32x32x16_f16. The MFMA's first operand is the weight row (n) and
+// its second the activation row (m): lane l then holds activation row l%32
+// and weight rows 8*(r/4) + 4*(l/32) + r%4 of register r, i.e. 4 consecutive
+// output columns per register group, so epilogues write 8-/16-byte vectors
+// and the partner columns n and n+32 of a 64-wide wave tile share a lane.
+#pragma once
+#include <algorithm>
+
+#include "common.hpp"
+
+namespace dhx {
+namespace gemm {
+
+constexpr int BK = 64;
+constexpr int LDK = BK + 8;  // LDS row pitch in halfs (144 B): conflict-free 16-byte fragment reads
+
+template <int BM_, int BN_, int WGM_, int WGN_>
+struct Tile {
+    static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_;
+    static constexpr int WAVES = WGM * WGN, THREADS = 64 * WAVES;
+    static constexpr int TM = BM / WGM, TN = BN / WGN;
+    static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile is a multiple of the 32x32 MFMA tile");
+    static constexpr int FM = TM / 32, FN = TN / 32;
+    static constexpr int STAGE_HALFS = (BM + BN) * LDK;
+    static constexpr int LDS_HALFS = 2 * STAGE_HALFS;
+    static constexpr int LDS_BYTES = LDS_HALFS * 2;
+};
+
+// Waits for this wave's LDS reads and writes, then joins the workgroup
+// barrier; global loads stay in flight. The memory clobber keeps the
+// compiler from moving LDS accesses across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+__device__ __forceinline__ half8_t zero8() {
+    half8_t z = {};
+    return z;
+}
+
+// Rows r0 .. r0+ROWS-1 of a row-major f16 [*][ld] matrix, 64 columns at
+// k_off + kt*64. Rows at or past `limit` re-load row limit-1: they only feed
+// output rows that are never stored, and an unconditional load keeps the
+// compiler's vmcnt accounting exact (a predicated load makes every later wait
+// drain the prefetches too).
+template <int ROWS, int THREADS>
+struct HalfTile {
+    static constexpr int CHUNKS = ROWS * BK / 8 / THREADS;
+    static_assert(ROWS * BK / 8 % THREADS == 0, "tile splits evenly over the workgroup");
+    half8_t r[CHUNKS];
+    __device__ __forceinline__ void load(const half_t* base, int ld, int r0, int limit, int k0, int tid) {
+#pragma unroll
+        for (int i = 0; i < CHUNKS; ++i) {
+            const int c = tid + i * THREADS, row = c >> 3, col = (c & 7) * 8;
+            const int m = min(r0 + row, limit - 1);
+            r[i] = *(const half8_t*)(base + (size_t)m * ld + k0 + col);
+        }
+    }
+    __device__ __forceinline__ void load_all(const half_t* base, int ld, int r0, int k0, int tid) {
+#pragma unroll
+        for (int i = 0; i < CHUNKS; ++i) {
+            const int c = tid + i * THREADS, row = c >> 3, col = (c & 7) * 8;
+            r[i] = *(const half8_t*)(base + (size_t)(r0 + row) * ld + k0 + col);
+        }
+    }
+    __device__ __forceinline__ void store(half_t* s, int tid) const {
+#pragma unroll
+        for (int i = 0; i < CHUNKS; ++i) {
+            const int c = tid + i * THREADS, row = c >> 3, col = (c & 7) * 8;
+            *(half8_t*)(s + row * LDK + col) = r[i];
+        }
+    }
+};
+
+// A operand: f16 activations [M][lda], rows m0 .. m0+BM-1.
+template <class T>
+struct ActRows {
+    HalfTile<T::BM, T::THREADS> t;
+    const half_t* a;
+    int lda, M, k_off;
+    __device__ __forceinline__ void load(int m0, int /*n0*/, int kt, int tid) {
+        t.load(a, lda, m0, M, k_off + kt * BK, tid);
+    }
+    __device__ __forceinline__ void store(half_t* s, int tid) const { t.store(s, tid); }
+};
+
+// Weight operand: rows n0 .. n0+BN-1 of W[N][ldw] (the launchers only use N
+// that are multiples of BN, so every row exists).
+template <class T>
+struct WeightRows {
+    HalfTile<T::BN, T::THREADS> t;
+    const half_t* w;
+    int ldw, k_off;
+    __device__ __forceinline__ void load(int /*m0*/, int n0, int kt, int tid) {
+        t.load_all(w, ldw, n0, k_off + kt * BK, tid);
+    }
+    __device__ __forceinline__ void store(half_t* s, int tid) const { t.store(s, tid); }
+};
+
+template <class T>
+struct Acc {
+    float16_t v[T::FN][T::FM];
+};
+
+// One 64-deep stage of MFMAs from LDS. Fragments are double-buffered in
+// registers: the reads for k-slice kk+1 are issued before the MFMAs of kk, so
+// LDS latency overlaps the matrix pipe instead of stalling each MFMA.
+template <class T>
+__device__ __forceinline__ void mma_stage(const half_t* stage, int tid, Acc<T>& acc) {
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave % T::WGM, wn = wave / T::WGM;
+    const int l32 = lane & 31, hi = lane >> 5;
+    const half_t* a_s = stage + (wm * T::TM + l32) * LDK + hi * 8;
+    const half_t* w_s = stage + (T::BM + wn * T::TN + l32) * LDK + hi * 8;
+    half8_t wf[2][T::FN], af[2][T::FM];
+    auto fetch = [&](int kk, int b) {
+#pragma unroll
+        for (int i = 0; i < T::FN; ++i) wf[b][i] = *(const half8_t*)(w_s + i * 32 * LDK + kk * 16);
+#pragma unroll
+        for (int j = 0; j < T::FM; ++j) af[b][j] = *(const half8_t*)(a_s + j * 32 * LDK + kk * 16);
+    };
+    fetch(0, 0);
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+        if (kk + 1 < BK / 16) fetch(kk + 1, (kk + 1) & 1);
+#pragma unroll
+        for (int i = 0; i < T::FN; ++i)
+#pragma unroll
+            for (int j = 0; j < T::FM; ++j) acc.v[i][j] = mfma32x32x16(wf[kk & 1][i], af[kk & 1][j], acc.v[i][j]);
+    }
+}
+
+// The workgroup's tile: hardware workgroup ids are dispatched round-robin
+// over the 8 XCDs (each with its own L2); the tile space (n fastest) is cut
+// into 8 contiguous chunks and XCD x takes chunk x, so the workgroups of one
+// XCD work on neighbouring tiles and share A rows and W in that XCD's L2.
+// The grid is the tile count rounded up to a multiple of 8; workgroups past
+// the end of their chunk have no tile.
+__device__ __forceinline__ int xcd_tile(int total) {
+    const int g = blockIdx.x, per = (total + 7) >> 3;
+    const int t = (g & 7) * per + (g >> 3);
+    return (g >> 3) < per && t < total ? t : -1;
+}
+
+// The pipelined K loop of one tile; k_tiles must be even (host-checked:
+// K % 128 == 0). The loaders take the tile origin (m0, n0) and the stage.
+template <class T, class AL, class WL>
+__device__ __forceinline__ void gemm_main(AL (&al)[2], WL (&wl)[2], int m0, int n0, int k_tiles, half_t* lds,
+                                          Acc<T>& acc) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < T::FN; ++i)
+#pragma unroll
+        for (int j = 0; j < T::FM; ++j) acc.v[i][j] = float16_t{};
+    half_t* const s0 = lds;
+    half_t* const s1 = lds + T::STAGE_HALFS;
+    const int last = k_tiles - 1;
+    al[0].load(m0, n0, 0, tid);
+    wl[0].load(m0, n0, 0, tid);
+    al[1].load(m0, n0, min(1, last), tid);
+    wl[1].load(m0, n0, min(1, last), tid);
+    al[0].store(s0, tid);
+    wl[0].store(s0 + T::BM * LDK, tid);
+    lds_barrier();
+    for (int kt = 0; kt < k_tiles; kt += 2) {
+        // s0 holds stage kt; register set 1 holds stage kt+1 (maybe in flight).
+        al[0].load(m0, n0, min(kt + 2, last), tid);
+        wl[0].load(m0, n0, min(kt + 2, last), tid);
+        mma_stage<T>(s0, tid, acc);
+        al[1].store(s1, tid);
+        wl[1].store(s1 + T::BM * LDK, tid);
+        lds_barrier();
+        al[1].load(m0, n0, min(kt + 3, last), tid);
+        wl[1].load(m0, n0, min(kt + 3, last), tid);
+        mma_stage<T>(s1, tid, acc);
+        if (kt + 2 < k_tiles) {
+            al[0].store(s0, tid);
+            wl[0].store(s0 + T::BM * LDK, tid);
+        }
+        lds_barrier();
+    }
+}
+
+// Runs the tile of this workgroup (if any) and its epilogue epi(acc, m0, n0).
+template <class T, class AL, class WL, class Epi>
+__device__ __forceinline__ void gemm_tile(AL (&al)[2], WL (&wl)[2], int n_tiles, int total_tiles, int k_tiles,
+                                          half_t* lds, Epi&& epi) {
+    const int t = xcd_tile(total_tiles);
+    if (t < 0) return;  // uniform per workgroup
+    const int n0 = (t % n_tiles) * T::BN, m0 = (t / n_tiles) * T::BM;
+    Acc<T> acc;
+    gemm_main<T>(al, wl, m0, n0, k_tiles, lds, acc);
+    epi(acc, m0, n0);
+}
+
+// Workgroups for a launch: one per tile (a persistent walk over several
+// tiles per resident workgroup measured slower: the hardware balances the
+// last wave of tiles better), rounded up to a multiple of 8 for xcd_tile.
+inline int tile_grid(int total_tiles) { return std::max(8, (total_tiles + 7) & ~7); }
+
+__device__ __forceinline__ float4_t group4(const float16_t& a, int g) {
+    return float4_t{a[4 * g], a[4 * g + 1], a[4 * g + 2], a[4 * g + 3]};
+}
+
+__device__ __forceinline__ half4_t to_half4(float4_t v) {
+    return half4_t{(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]};
+}
+
+__device__ __forceinline__ float4_t ld4(const float* p) { return *(const float4_t*)p; }
+
+// Position of this lane's outputs: row m_base + 32j + l32, columns
+// n_base + 32i + 8g + 4hi .. +3 for register group g of acc.v[i][j].
+template <class T>
+struct Frag {
+    int l32, hi, m_base, n_base;
+    __device__ __forceinline__ Frag(int m0, int n0) {
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        l32 = lane & 31;
+        hi = lane >> 5;
+        m_base = m0 + (wave % T::WGM) * T::TM;
+        n_base = n0 + (wave / T::WGM) * T::TN;
+    }
+    __device__ __forceinline__ int row(int j) const { return m_base + j * 32 + l32; }
+    __device__ __forceinline__ int col(int i, int g) const { return n_base + i * 32 + g * 8 + hi * 4; }
+};
+
+template <class T>
+inline int tiles_for(int rows, int n) {
+    return (n / T::BN) * ((rows + T::BM - 1) / T::BM);
+}
+
+}  // namespace gemm
+}  // namespace dhx

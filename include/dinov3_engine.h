@@ -44,7 +44,8 @@ typedef struct dhx_region {
  *   DHX_K_SPLITK        s = {rows, k, splits}        b = {a f16, w f16 [384][k], partials f32 [splits][rows][384]}
  *   DHX_K_SPLITK_REDUCE s = {rows, splits}           b = {partials f32, b f32, ls f32, x f16}
  * q and k are [images][6][tpad][64] f16, vt is [images][6][64][tpad] f16,
- * tpad a multiple of 128 >= T = grid*grid + 5. Every binding's size is
+ * tpad a multiple of 128 >= T = grid*grid + 5; k (and k / splits) a multiple
+ * of 128 (the GEMM K loop runs stages of 64 in pairs). Every binding's size is
  * checked against these shapes before anything is launched or recorded. */
 enum {
     DHX_K_PATCH_EMBED = 0,
