@@ -15,6 +15,7 @@ oracle timed on this host as a baseline.
 import argparse
 import json
 import os
+import re
 import sys
 import tempfile
 import time
@@ -53,6 +54,20 @@ def kernel_work(name, b, T, G):
     if name == "splitk_reduce":
         return 0, 4 * r * H * f32 + 2 * r * H * f16
     raise KeyError(name)
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "forward_b64_traffic.md")
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` at batch 64, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (calibrated there), or None."""
+    try:
+        text = open(TRAFFIC_FILE).read()
+    except OSError:
+        return None
+    m = re.search(r"traffic\[" + re.escape(kernel) + r"\] = (\d+) bytes/launch", text)
+    return int(m.group(1)) if m else None
 
 
 def timed_replays(model, b, steps):
@@ -129,12 +144,14 @@ def main():
         sec32 = timed_replays(model, 32, args.steps)
 
         # Per-launch device time (HIP events on the model's stream).
-        launches = model.launch_timings(b, iters=20, splitk=mode)
+        launches = model.launch_timings(b, iters=20)
         kernels = {}
         for i, (name, ms) in enumerate(launches):
+            name = {"patch_embed_stats": "patch_embed", "qkv_rope_ln": "qkv_rope", "resid_stats": "resid",
+                    "swiglu_ln": "swiglu", "splitk_reduce_stats": "splitk_reduce"}.get(name, name)
             if name == "resid":
-                # the o-projection (k = 384) precedes the down projection (k = 1536) in each block
-                name = "resid_1536" if launches[i - 1][0] == "swiglu" else "resid_384"
+                # the down projection (k = 1536) follows the SwiGLU GEMM; the o-projection (k = 384) follows attention
+                name = "resid_1536" if launches[i - 1][0].startswith("swiglu") else "resid_384"
             k = kernels.setdefault(name, {"count": 0, "ms": 0.0})
             k["count"] += 1
             k["ms"] += ms
@@ -158,7 +175,8 @@ def main():
         else:
             roof = {"kernel": dom["kernel"], "bound": "hbm", "achieved": dom["gbs"], "peak": PEAK_GBS,
                     "unit": "GB/s", "frac": round(dom["gbs"] / PEAK_GBS, 4)}
-        roof["traffic"] = None
+        roof["traffic"] = measured_traffic(dom["kernel"]) if b == 64 else None
+        roof["algorithmic_bytes"] = nbytes
         roof["avg_us"] = dom["avg_us"]
         model.close()
 

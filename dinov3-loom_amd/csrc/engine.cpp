@@ -88,12 +88,16 @@ Need required(const dhx_launch& l) {
     auto positive = [](uint64_t v, const char* what) {
         if (v == 0) throw dhx::Error(std::string(what) + " must be positive");
     };
+    const uint64_t S = dhx::kStatFloats * 4;  // stats bytes per row
     switch (l.kernel) {
-        case DHX_K_PATCH_EMBED: {
+        case DHX_K_PATCH_EMBED:
+        case DHX_K_PATCH_EMBED_STATS: {
             positive(s[0], "images");
             positive(s[1], "grid");
             const uint64_t side = 16ull * s[1], T = tokens_for(s[1]);
-            return {5, {s[0] * 3 * side * side * 4, H * 768 * 2, H * 4, 5 * H * 4, s[0] * T * H * 2}};
+            const uint64_t px = s[0] * 3 * side * side * 4, x = s[0] * T * H * 2;
+            if (l.kernel == DHX_K_PATCH_EMBED) return {5, {px, H * 768 * 2, H * 4, 5 * H * 4, x}};
+            return {7, {px, H * 768 * 2, H * 4, 5 * H * 4, 5 * S, x, s[0] * T * S}};
         }
         case DHX_K_LAYERNORM:
         case DHX_K_LAYERNORM_F32: {
@@ -102,6 +106,7 @@ Need required(const dhx_launch& l) {
             return {4, {s[0] * H * 2, H * 4, H * 4, s[0] * H * out}};
         }
         case DHX_K_QKV_ROPE:
+        case DHX_K_QKV_ROPE_LN:
         case DHX_K_ATTENTION: {
             positive(s[0], "images");
             positive(s[1], "grid");
@@ -109,16 +114,26 @@ Need required(const dhx_launch& l) {
             if (s[2] % 128 != 0 || s[2] < T) throw dhx::Error("tpad must be a multiple of 128 covering every token");
             const uint64_t heads = s[0] * dhx::kHeads * (uint64_t)s[2] * dhx::kHeadDim * 2;
             if (l.kernel == DHX_K_ATTENTION) return {4, {heads, heads, heads, s[0] * T * H * 2}};
-            return {8, {s[0] * T * H * 2, 3 * H * H * 2, 3 * H * 4, P * 64 * 4, P * 64 * 4, heads, heads, heads}};
+            if (l.kernel == DHX_K_QKV_ROPE)
+                return {8, {s[0] * T * H * 2, 3 * H * H * 2, 3 * H * 4, P * 64 * 4, P * 64 * 4, heads, heads, heads}};
+            return {10, {s[0] * T * H * 2, s[0] * T * S, 3 * H * H * 2, 3 * H * 4, 3 * H * 4, P * 64 * 4, P * 64 * 4,
+                         heads, heads, heads}};
         }
-        case DHX_K_RESID: {
+        case DHX_K_RESID:
+        case DHX_K_RESID_STATS: {
             positive(s[0], "rows");
             if (s[1] == 0 || s[1] % 128 != 0) throw dhx::Error("k must be a positive multiple of 128");
-            return {5, {s[0] * (uint64_t)s[1] * 2, H * s[1] * 2, H * 4, H * 4, s[0] * H * 2}};
+            std::vector<uint64_t> b = {s[0] * (uint64_t)s[1] * 2, H * s[1] * 2, H * 4, H * 4, s[0] * H * 2};
+            if (l.kernel == DHX_K_RESID_STATS) b.push_back(s[0] * S);
+            return {(uint32_t)b.size(), b};
         }
         case DHX_K_SWIGLU:
             positive(s[0], "rows");
             return {4, {s[0] * H * 2, 2ull * dhx::kFF * H * 2, 2ull * dhx::kFF * 4, s[0] * (uint64_t)dhx::kFF * 2}};
+        case DHX_K_SWIGLU_LN:
+            positive(s[0], "rows");
+            return {6, {s[0] * H * 2, s[0] * S, 2ull * dhx::kFF * H * 2, 2ull * dhx::kFF * 4, 2ull * dhx::kFF * 4,
+                        s[0] * (uint64_t)dhx::kFF * 2}};
         case DHX_K_SPLITK: {
             positive(s[0], "rows");
             positive(s[2], "splits");
@@ -126,9 +141,13 @@ Need required(const dhx_launch& l) {
             return {3, {s[0] * (uint64_t)s[1] * 2, H * s[1] * 2, (uint64_t)s[2] * s[0] * H * 4}};
         }
         case DHX_K_SPLITK_REDUCE:
+        case DHX_K_SPLITK_REDUCE_STATS: {
             positive(s[0], "rows");
             positive(s[1], "splits");
-            return {4, {(uint64_t)s[1] * s[0] * H * 4, H * 4, H * 4, s[0] * H * 2}};
+            std::vector<uint64_t> b = {(uint64_t)s[1] * s[0] * H * 4, H * 4, H * 4, s[0] * H * 2};
+            if (l.kernel == DHX_K_SPLITK_REDUCE_STATS) b.push_back(s[0] * S);
+            return {(uint32_t)b.size(), b};
+        }
         default:
             throw dhx::Error("unknown kernel id " + std::to_string(l.kernel));
     }
@@ -155,25 +174,38 @@ hipError_t launch_one(dhx_engine* e, const dhx_launch& l) {
     auto F = [&](int i) { return static_cast<const float*>(P(i)); };
     auto Hf = [&](int i) { return static_cast<half_t*>(P(i)); };
     const uint32_t* s = l.scalars;
+    auto Fm = [&](int i) { return static_cast<float*>(P(i)); };
     switch (l.kernel) {
         case DHX_K_PATCH_EMBED:
             return launch_patch_embed({F(0), Hf(1), F(2), F(3), Hf(4), (int)s[0], (int)s[1]}, e->stream);
+        case DHX_K_PATCH_EMBED_STATS:
+            return launch_patch_embed({F(0), Hf(1), F(2), F(3), Hf(5), (int)s[0], (int)s[1], F(4), Fm(6)}, e->stream);
         case DHX_K_LAYERNORM:
         case DHX_K_LAYERNORM_F32:
             return launch_layernorm({Hf(0), F(1), F(2), P(3), (int)s[0], l.kernel == DHX_K_LAYERNORM_F32}, e->stream);
         case DHX_K_QKV_ROPE:
             return launch_qkv_rope({Hf(0), Hf(1), F(2), F(3), F(4), Hf(5), Hf(6), Hf(7), (int)s[0], (int)s[1], (int)s[2]},
                                    e->stream);
+        case DHX_K_QKV_ROPE_LN:
+            return launch_qkv_rope({Hf(0), Hf(2), F(4), F(5), F(6), Hf(7), Hf(8), Hf(9), (int)s[0], (int)s[1], (int)s[2],
+                                    F(1), F(3)},
+                                   e->stream);
         case DHX_K_ATTENTION:
             return launch_attention({Hf(0), Hf(1), Hf(2), Hf(3), (int)s[0], (int)tokens_for(s[1]), (int)s[2]}, e->stream);
         case DHX_K_RESID:
             return launch_resid({Hf(0), Hf(1), F(2), F(3), Hf(4), (int)s[0], (int)s[1]}, e->stream);
+        case DHX_K_RESID_STATS:
+            return launch_resid({Hf(0), Hf(1), F(2), F(3), Hf(4), (int)s[0], (int)s[1], Fm(5)}, e->stream);
         case DHX_K_SWIGLU:
             return launch_swiglu({Hf(0), Hf(1), F(2), Hf(3), (int)s[0]}, e->stream);
+        case DHX_K_SWIGLU_LN:
+            return launch_swiglu({Hf(0), Hf(2), F(4), Hf(5), (int)s[0], F(1), F(3)}, e->stream);
         case DHX_K_SPLITK:
             return launch_splitk({Hf(0), Hf(1), (float*)P(2), (int)s[0], (int)s[1], (int)s[2]}, e->stream);
         case DHX_K_SPLITK_REDUCE:
             return launch_splitk_reduce({F(0), F(1), F(2), Hf(3), (int)s[0], (int)s[1]}, e->stream);
+        case DHX_K_SPLITK_REDUCE_STATS:
+            return launch_splitk_reduce({F(0), F(1), F(2), Hf(3), (int)s[0], (int)s[1], Fm(4)}, e->stream);
         default:
             return hipErrorInvalidValue;
     }

@@ -34,7 +34,13 @@ __device__ __forceinline__ half8_t zero8() {
 __global__ __launch_bounds__(kThreads) void attention_kernel(AttentionArgs p) {
     __shared__ half_t sK[2][KB * KLD];
     __shared__ half_t sV[2][kHeadDim * KLD];
-    const int qb = blockIdx.x, head = blockIdx.y, img = blockIdx.z;
+    // 1-D grid, XCD-aware: the tile space (query block fastest, then head,
+    // then image) is cut into 8 contiguous chunks, one per XCD, so the query
+    // blocks of one (image, head) share K and V in that XCD's L2.
+    const int nqb = (p.tokens + QB - 1) / QB, total = nqb * kHeads * p.images;
+    const int per = (total + 7) >> 3, g = blockIdx.x, t = (g & 7) * per + (g >> 3);
+    if ((g >> 3) >= per || t >= total) return;  // uniform per workgroup
+    const int qb = t % nqb, head = (t / nqb) % kHeads, img = t / (nqb * kHeads);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l32 = lane & 31, hi = lane >> 5;
     const int T = p.tokens;
@@ -151,8 +157,8 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttentionArgs p) {
 }  // namespace
 
 hipError_t launch_attention(const AttentionArgs& a, hipStream_t s) {
-    const dim3 grid((a.tokens + QB - 1) / QB, kHeads, a.images);
-    hipLaunchKernelGGL(attention_kernel, grid, dim3(kThreads), 0, s, a);
+    const int total = (a.tokens + QB - 1) / QB * kHeads * a.images;
+    hipLaunchKernelGGL(attention_kernel, dim3((total + 7) & ~7), dim3(kThreads), 0, s, a);
     return hipGetLastError();
 }
 

@@ -42,15 +42,24 @@ __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcp
 // silu(g) = g / (1 + e^-g), with e^-g evaluated as 2^(-g * log2 e) on v_exp_f32.
 __device__ __forceinline__ float silu(float g) { return g * fast_rcp(1.0f + fast_exp2(-g * kLog2e)); }
 
-// Workgroups are dispatched round-robin over the 8 XCDs (each with its own
-// L2). Remap the hardware id so that consecutive logical ids share an XCD:
-// logical tiles [k*per, (k+1)*per) land on XCD k. Ids past the last full
-// group of 8 keep their identity.
-__device__ __forceinline__ int xcd_remap(int hw_id, int total) {
-    const int full = total & ~7;
-    if (hw_id >= full) return hw_id;
-    const int per = full >> 3;
-    return (hw_id & 7) * per + (hw_id >> 3);
+// LayerNorm statistics of one row from its six 64-column partials
+// (mean_k, M2_k): mean = avg mean_k, M2 = sum M2_k + 64 * sum (mean_k -
+// mean)^2 (Chan et al.'s pairwise combination), var = M2 / 384, eps 1e-5.
+struct RowNorm {
+    float mean, rstd;
+};
+
+__device__ __forceinline__ RowNorm row_norm(const float* stats, size_t row) {
+    const float4_t* p = (const float4_t*)(stats + row * 12);
+    const float4_t a = p[0], b = p[1], c = p[2];
+    const float mk[6] = {a[0], a[2], b[0], b[2], c[0], c[2]};
+    const float m2 = (a[1] + a[3]) + (b[1] + b[3]) + (c[1] + c[3]);
+    const float mean = (((mk[0] + mk[1]) + (mk[2] + mk[3])) + (mk[4] + mk[5])) * (1.0f / 6.0f);
+    float dev = 0.f;
+#pragma unroll
+    for (int i = 0; i < 6; ++i) dev += (mk[i] - mean) * (mk[i] - mean);
+    const float var = (m2 + 64.0f * dev) * (1.0f / kHidden);
+    return RowNorm{mean, rsqrtf(var + 1e-5f)};
 }
 
 }  // namespace dhx

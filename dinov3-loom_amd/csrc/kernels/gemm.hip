@@ -23,21 +23,27 @@ hipError_t launch(void (*kernel)(Args), int tiles, const Args& a, hipStream_t s)
 }  // namespace
 
 hipError_t launch_patch_embed(const PatchEmbedArgs& a, hipStream_t s) {
-    return launch<PatchTile>(gemm::patch_embed_kernel<PatchTile>,
-                             tiles_for<PatchTile>(a.images * a.grid * a.grid, kHidden), a, s);
+    const int tiles = tiles_for<PatchTile>(a.images * a.grid * a.grid, kHidden);
+    return a.stats ? launch<PatchTile>(gemm::patch_embed_kernel<PatchTile, true>, tiles, a, s)
+                   : launch<PatchTile>(gemm::patch_embed_kernel<PatchTile, false>, tiles, a, s);
 }
 
 hipError_t launch_qkv_rope(const QkvArgs& a, hipStream_t s) {
-    return launch<QkvTile>(gemm::qkv_rope_kernel<QkvTile>,
-                           tiles_for<QkvTile>(a.images * (a.grid * a.grid + kPrefix), 3 * kHidden), a, s);
+    const int tiles = tiles_for<QkvTile>(a.images * (a.grid * a.grid + kPrefix), 3 * kHidden);
+    return a.stats ? launch<QkvTile>(gemm::qkv_rope_kernel<QkvTile, true>, tiles, a, s)
+                   : launch<QkvTile>(gemm::qkv_rope_kernel<QkvTile, false>, tiles, a, s);
 }
 
 hipError_t launch_resid(const ResidArgs& a, hipStream_t s) {
-    return launch<ResidTile>(gemm::resid_kernel<ResidTile>, tiles_for<ResidTile>(a.rows, kHidden), a, s);
+    const int tiles = tiles_for<ResidTile>(a.rows, kHidden);
+    return a.stats ? launch<ResidTile>(gemm::resid_kernel<ResidTile, true>, tiles, a, s)
+                   : launch<ResidTile>(gemm::resid_kernel<ResidTile, false>, tiles, a, s);
 }
 
 hipError_t launch_swiglu(const SwigluArgs& a, hipStream_t s) {
-    return launch<SwigluTile>(gemm::swiglu_kernel<SwigluTile>, tiles_for<SwigluTile>(a.rows, 2 * kFF), a, s);
+    const int tiles = tiles_for<SwigluTile>(a.rows, 2 * kFF);
+    return a.stats ? launch<SwigluTile>(gemm::swiglu_kernel<SwigluTile, true>, tiles, a, s)
+                   : launch<SwigluTile>(gemm::swiglu_kernel<SwigluTile, false>, tiles, a, s);
 }
 
 hipError_t launch_splitk(const SplitKArgs& a, hipStream_t s) {

@@ -45,9 +45,35 @@ struct PatchRows {
     }
 };
 
-// Patch embedding + CLS/register scatter into the f16 residual stream x.
-template <class T>
+// Writes this wave's (mean, M2) partial of row m over its 64 columns: the
+// lane holds 32 of them (v, already rounded to the f16 values stored in x),
+// its partner lane l ^ 32 the other 32. Both partners must call this.
+__device__ __forceinline__ void slot_stats(float* stats, size_t m, int slot, const float4_t (&v)[2][4], int hi) {
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) s += (v[i][g][0] + v[i][g][1]) + (v[i][g][2] + v[i][g][3]);
+    s += __shfl_xor(s, 32, 64);
+    const float mean = s * (1.0f / 64.0f);
+    float q = 0.f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) q += (v[i][g][e] - mean) * (v[i][g][e] - mean);
+    q += __shfl_xor(q, 32, 64);
+    if (hi == 0) *(float2_t*)(stats + m * kStatFloats + slot * 2) = float2_t{mean, q};
+}
+
+__device__ __forceinline__ float4_t widen(half4_t h) { return float4_t{(float)h[0], (float)h[1], (float)h[2], (float)h[3]}; }
+
+// Patch embedding + CLS/register scatter into the f16 residual stream x
+// (with STATS, also the LayerNorm row statistics of x).
+template <class T, bool STATS>
 __global__ __launch_bounds__(T::THREADS) void patch_embed_kernel(PatchEmbedArgs p) {
+    static_assert(!STATS || T::TN == 64, "one statistics slot per wave");
     __shared__ __attribute__((aligned(16))) half_t lds[T::LDS_HALFS];
     const int P = p.grid * p.grid, Tok = P + kPrefix, M = p.images * P;
     constexpr int NT = kHidden / T::BN;
@@ -61,29 +87,43 @@ __global__ __launch_bounds__(T::THREADS) void patch_embed_kernel(PatchEmbedArgs 
             const int m = f.row(j);
             if (m >= M) continue;
             const int img = m / P, patch = m - img * P;
-            half_t* dst = p.x + ((size_t)img * Tok + kPrefix + patch) * kHidden;
+            const size_t row = (size_t)img * Tok + kPrefix + patch;
+            half_t* dst = p.x + row * kHidden;
+            float4_t v[T::FN][4];
 #pragma unroll
             for (int i = 0; i < T::FN; ++i)
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const int n = f.col(i, g);
-                    *(half4_t*)(dst + n) = to_half4(group4(acc.v[i][j], g) + ld4(p.bias + n));
+                    const half4_t h = to_half4(group4(acc.v[i][j], g) + ld4(p.bias + n));
+                    *(half4_t*)(dst + n) = h;
+                    v[i][g] = widen(h);
                 }
+            if constexpr (STATS) slot_stats(p.stats, row, f.n_base / 64, v, f.hi);
         }
         // CLS + registers of every image whose first patch row lies in this tile.
         const int m_end = min(m0 + T::BM, M);
-        for (int img = (m0 + P - 1) / P; img * P < m_end; ++img)
+        for (int img = (m0 + P - 1) / P; img * P < m_end; ++img) {
             for (int idx = threadIdx.x; idx < kPrefix * T::BN; idx += T::THREADS) {
                 const int row = idx / T::BN, col = n0 + idx % T::BN;
                 p.x[((size_t)img * Tok + row) * kHidden + col] = (half_t)p.prefix[row * kHidden + col];
             }
+            if constexpr (STATS) {
+                constexpr int slots = T::BN / 64;
+                for (int idx = threadIdx.x; idx < kPrefix * slots * 2; idx += T::THREADS) {
+                    const int row = idx / (slots * 2), e = idx % (slots * 2);
+                    const int off = (n0 / 64) * 2 + e;
+                    p.stats[((size_t)img * Tok + row) * kStatFloats + off] = p.prefix_stats[row * kStatFloats + off];
+                }
+            }
+        }
     });
 }
 
 // QKV + bias + 2D RoPE. A wave's 64 columns are exactly one head of q, k or
 // v, so channel c and its rotation partner c+32 are acc.v[0] / acc.v[1] of
 // the same lane. q, k are written head-major, v transposed.
-template <class T>
+template <class T, bool LN>
 __global__ __launch_bounds__(T::THREADS) void qkv_rope_kernel(QkvArgs p) {
     static_assert(T::TN == kHeadDim, "one head per wave");
     __shared__ __attribute__((aligned(16))) half_t lds[T::LDS_HALFS];
@@ -101,11 +141,18 @@ __global__ __launch_bounds__(T::THREADS) void qkv_rope_kernel(QkvArgs p) {
             const int img = m / Tok, tok = m - img * Tok;
             const size_t bh = (size_t)img * kHeads + head;
             const bool rotate = part < 2 && tok >= kPrefix;
+            RowNorm rn{0.f, 1.f};
+            if constexpr (LN) rn = row_norm(p.stats, m);
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int c = g * 8 + f.hi * 4;  // channel in the head (0..31); partner c + 32
-                float4_t lo = group4(acc.v[0][j], g) + ld4(p.bias + f.n_base + c);
-                float4_t up = group4(acc.v[1][j], g) + ld4(p.bias + f.n_base + 32 + c);
+                float4_t lo = group4(acc.v[0][j], g), up = group4(acc.v[1][j], g);
+                if constexpr (LN) {
+                    lo = (lo - rn.mean * ld4(p.wsum + f.n_base + c)) * rn.rstd;
+                    up = (up - rn.mean * ld4(p.wsum + f.n_base + 32 + c)) * rn.rstd;
+                }
+                lo += ld4(p.bias + f.n_base + c);
+                up += ld4(p.bias + f.n_base + 32 + c);
                 if (rotate) {
                     const float* cs = p.cos + (tok - kPrefix) * kHeadDim;
                     const float* sn = p.sin + (tok - kPrefix) * kHeadDim;
@@ -131,9 +178,11 @@ __global__ __launch_bounds__(T::THREADS) void qkv_rope_kernel(QkvArgs p) {
     });
 }
 
-// Residual GEMM: x += ls * (A W^T + b), in place on the f16 residual stream.
-template <class T>
+// Residual GEMM: x += ls * (A W^T + b), in place on the f16 residual stream
+// (with STATS, also the LayerNorm row statistics of the updated x).
+template <class T, bool STATS>
 __global__ __launch_bounds__(T::THREADS) void resid_kernel(ResidArgs p) {
+    static_assert(!STATS || T::TN == 64, "one statistics slot per wave");
     __shared__ __attribute__((aligned(16))) half_t lds[T::LDS_HALFS];
     constexpr int NT = kHidden / T::BN;
     ActRows<T> al[2] = {{{}, p.a, p.k, p.rows, 0}, {{}, p.a, p.k, p.rows, 0}};
@@ -146,16 +195,18 @@ __global__ __launch_bounds__(T::THREADS) void resid_kernel(ResidArgs p) {
             const int m = f.row(j);
             if (m >= p.rows) continue;
             half_t* xr = p.x + (size_t)m * kHidden;
+            float4_t v[T::FN][4];
 #pragma unroll
             for (int i = 0; i < T::FN; ++i)
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const int n = f.col(i, g);
-                    const half4_t old = *(const half4_t*)(xr + n);
                     const float4_t upd = (group4(acc.v[i][j], g) + ld4(p.bias + n)) * ld4(p.ls + n);
-                    const float4_t xo = float4_t{(float)old[0], (float)old[1], (float)old[2], (float)old[3]};
-                    *(half4_t*)(xr + n) = to_half4(xo + upd);
+                    const half4_t h = to_half4(widen(*(const half4_t*)(xr + n)) + upd);
+                    *(half4_t*)(xr + n) = h;
+                    v[i][g] = widen(h);
                 }
+            if constexpr (STATS) slot_stats(p.stats, m, f.n_base / 64, v, f.hi);
         }
     });
 }
@@ -163,7 +214,7 @@ __global__ __launch_bounds__(T::THREADS) void resid_kernel(ResidArgs p) {
 // SwiGLU dual GEMM. W rows are packed as blocks of 32 gate rows followed by
 // the 32 matching up rows, so a wave's 64 columns are 32 gate and 32 up
 // columns of the same 32 outputs.
-template <class T>
+template <class T, bool LN>
 __global__ __launch_bounds__(T::THREADS) void swiglu_kernel(SwigluArgs p) {
     static_assert(T::TN == 64, "gate/up pair per wave");
     __shared__ __attribute__((aligned(16))) half_t lds[T::LDS_HALFS];
@@ -179,11 +230,18 @@ __global__ __launch_bounds__(T::THREADS) void swiglu_kernel(SwigluArgs p) {
             const int m = f.row(j);
             if (m >= p.rows) continue;
             half_t* dst = p.act + (size_t)m * kFF + out_base;
+            RowNorm rn{0.f, 1.f};
+            if constexpr (LN) rn = row_norm(p.stats, m);
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int c = g * 8 + f.hi * 4;
-                const float4_t gate = group4(acc.v[0][j], g) + ld4(p.bias + f.n_base + c);
-                const float4_t up = group4(acc.v[1][j], g) + ld4(p.bias + f.n_base + 32 + c);
+                float4_t gate = group4(acc.v[0][j], g), up = group4(acc.v[1][j], g);
+                if constexpr (LN) {
+                    gate = (gate - rn.mean * ld4(p.wsum + f.n_base + c)) * rn.rstd;
+                    up = (up - rn.mean * ld4(p.wsum + f.n_base + 32 + c)) * rn.rstd;
+                }
+                gate += ld4(p.bias + f.n_base + c);
+                up += ld4(p.bias + f.n_base + 32 + c);
                 const float4_t y = float4_t{silu(gate[0]), silu(gate[1]), silu(gate[2]), silu(gate[3])} * up;
                 *(half4_t*)(dst + c) = to_half4(y);
             }

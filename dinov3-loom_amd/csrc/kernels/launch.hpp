@@ -30,11 +30,27 @@ struct PatchEmbedArgs {
     half_t* x;
     int images;
     int grid;  // patches per side G; image side 16*G, T = G*G + 5
+    // Optional (both or neither): row statistics of x for a fused LayerNorm
+    // consumer; prefix_stats holds those of the 5 prefix rows [5][6][2].
+    const float* prefix_stats = nullptr;
+    float* stats = nullptr;
 };
+
+// Row statistics of the residual stream x for LayerNorm fused into the next
+// GEMM: stats[row][slot][2] = (mean, M2) of the f16 values of x in columns
+// 64*slot .. 64*slot+63, slot 0..5 (M2 = sum of squared deviations from that
+// slot's mean). A consumer combines the six slots (Chan et al.'s pairwise
+// update) into the row mean and variance.
+constexpr int kStatSlots = kHidden / 64;
+constexpr int kStatFloats = 2 * kStatSlots;
 
 // h [rows][384] f16 . Wqkv[1152][384]^T + b, 2D RoPE on q and k of patch
 // tokens, written head-major: q, k [images][6][tpad][64]; v transposed as
 // vt [images][6][64][tpad].
+// With stats == nullptr: h = LN1(x) is given and out = h.W^T + bias. With
+// stats: h is the raw residual x, w holds W' = gamma (.) W (per input
+// channel), wsum[n] = sum_k W'[n][k] and bias holds t = b + beta.W^T, so
+// out = rstd * (x.W'^T - mean * wsum) + t = LN(x).W^T + b.
 struct QkvArgs {
     const half_t* h;
     const half_t* w;
@@ -47,6 +63,8 @@ struct QkvArgs {
     int images;
     int grid;
     int tpad;
+    const float* stats = nullptr;
+    const float* wsum = nullptr;
 };
 
 // softmax(q k^T / 8) v per (image, head) over that image's T tokens;
@@ -70,16 +88,20 @@ struct ResidArgs {
     half_t* x;
     int rows;
     int k;
+    float* stats = nullptr;  // optional: row statistics of the updated x
 };
 
 // act[rows][1536] = silu(h.Wg^T + bg) * (h.Wu^T + bu); W and b are packed
 // with gate and up rows interleaved in blocks of 32.
+// stats / wsum: LayerNorm fused as in QkvArgs.
 struct SwigluArgs {
     const half_t* h;
     const half_t* w;
     const float* bias;
     half_t* act;
     int rows;
+    const float* stats = nullptr;
+    const float* wsum = nullptr;
 };
 
 // partials[s][rows][384] = a[:, s*k/splits ...] . W[:, s*k/splits ...]^T (f32).
@@ -100,6 +122,7 @@ struct ReduceArgs {
     half_t* x;
     int rows;
     int splits;
+    float* stats = nullptr;  // optional: row statistics of the updated x
 };
 
 hipError_t launch_layernorm(const LayerNormArgs& a, hipStream_t s);

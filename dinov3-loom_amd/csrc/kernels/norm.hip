@@ -59,19 +59,49 @@ __global__ __launch_bounds__(kThreads) void layernorm_kernel(LayerNormArgs p) {
     }
 }
 
-// x += ls * (sum_s partials[s] + b), four channels per thread.
+// x += ls * (sum_s partials[s] + b): one wave per row, lanes 0..47 own 8
+// channels each (8 lanes per 64-column statistics slot). With STATS, the
+// slot partials (mean, M2) of the updated f16 row are written as well.
+template <bool STATS>
 __global__ __launch_bounds__(kThreads) void splitk_reduce_kernel(ReduceArgs p) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    if (row >= p.rows) return;  // the whole wave leaves together
+    const bool active = lane < kHidden / 8;
     const size_t total = (size_t)p.rows * kHidden;
-    const size_t i = ((size_t)blockIdx.x * kThreads + threadIdx.x) * 4;
-    if (i >= total) return;
-    const int n = (int)(i % kHidden);
-    float4_t acc = *(const float4_t*)(p.partials + i);
-    for (int s = 1; s < p.splits; ++s) acc += *(const float4_t*)(p.partials + (size_t)s * total + i);
-    acc = (acc + *(const float4_t*)(p.bias + n)) * *(const float4_t*)(p.ls + n);
-    half4_t x = *(const half4_t*)(p.x + i);
-    half4_t y = {(half_t)((float)x[0] + acc[0]), (half_t)((float)x[1] + acc[1]),
-                 (half_t)((float)x[2] + acc[2]), (half_t)((float)x[3] + acc[3])};
-    *(half4_t*)(p.x + i) = y;
+    const int c = (active ? lane : 0) * 8;
+    const size_t i = (size_t)row * kHidden + c;
+    float y[8];
+    float4_t a0 = *(const float4_t*)(p.partials + i), a1 = *(const float4_t*)(p.partials + i + 4);
+    for (int s = 1; s < p.splits; ++s) {
+        a0 += *(const float4_t*)(p.partials + (size_t)s * total + i);
+        a1 += *(const float4_t*)(p.partials + (size_t)s * total + i + 4);
+    }
+    a0 = (a0 + *(const float4_t*)(p.bias + c)) * *(const float4_t*)(p.ls + c);
+    a1 = (a1 + *(const float4_t*)(p.bias + c + 4)) * *(const float4_t*)(p.ls + c + 4);
+    const half8_t x = *(const half8_t*)(p.x + i);
+    half8_t h;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        h[e] = (half_t)((float)x[e] + (e < 4 ? a0[e] : a1[e - 4]));
+        y[e] = (float)h[e];
+    }
+    if (active) *(half8_t*)(p.x + i) = h;
+    if constexpr (STATS) {
+        float s = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s += y[e];
+#pragma unroll
+        for (int o = 1; o < 8; o <<= 1) s += __shfl_xor(s, o, kWave);
+        const float mean = s * (1.0f / 64.0f);
+        float q = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) q += (y[e] - mean) * (y[e] - mean);
+#pragma unroll
+        for (int o = 1; o < 8; o <<= 1) q += __shfl_xor(q, o, kWave);
+        if (active && (lane & 7) == 0)
+            *(float2_t*)(p.stats + (size_t)row * kStatFloats + (lane >> 3) * 2) = float2_t{mean, q};
+    }
 }
 
 }  // namespace
@@ -83,9 +113,9 @@ hipError_t launch_layernorm(const LayerNormArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_splitk_reduce(const ReduceArgs& a, hipStream_t s) {
-    const size_t quads = (size_t)a.rows * kHidden / 4;
-    const int blocks = (int)((quads + kThreads - 1) / kThreads);
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(kThreads), 0, s, a);
+    const int blocks = (a.rows + kRowsPerBlock - 1) / kRowsPerBlock;
+    if (a.stats) hipLaunchKernelGGL(splitk_reduce_kernel<true>, dim3(blocks), dim3(kThreads), 0, s, a);
+    else hipLaunchKernelGGL(splitk_reduce_kernel<false>, dim3(blocks), dim3(kThreads), 0, s, a);
     return hipGetLastError();
 }
 

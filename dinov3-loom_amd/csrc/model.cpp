@@ -94,10 +94,11 @@ public:
         const uint64_t B = opts.max_batch, r = B * tokens_;
         const uint64_t heads = B * 6 * tpad_ * 64 * 2;
         // x, h, attn and act are f16; q/k/v^T are f16 head-major (padded rows
-        // stay zero); out, the NCHW images and the split-K slabs are f32.
+        // stay zero); out, the NCHW images, the split-K slabs and the
+        // LayerNorm row statistics of x are f32.
         const uint64_t sizes[kBuffers] = {r * kHiddenU * 2, r * kHiddenU * 2, heads, heads, heads, r * kHiddenU * 2,
                                           r * 1536 * 2,     r * kHiddenU * 4, B * image_elems_ * 4,
-                                          (uint64_t)kSplits * r * kHiddenU * 4};
+                                          (uint64_t)kSplits * r * kHiddenU * 4, r * 12 * 4};
         for (int i = 0; i < kBuffers; ++i) check(dhx_allocate(e, sizes[i], &a_[i]), e);
         check(dhx_reserve_readback(e, B * tokens_ * kHiddenU * 4), e);
     }
@@ -109,6 +110,11 @@ public:
     void set_splitk(int mode) {
         if (mode != 0 && mode != 1) throw Error("split-K mode must be 0 or 1");
         splitk_ = mode;  // graphs are keyed by (batch, variant); see key()
+    }
+
+    void set_layernorm_fusion(int on) {
+        if (on != 0 && on != 1) throw Error("layernorm fusion must be 0 or 1");
+        fused_ln_ = on;
     }
 
     // lib.rs:90-114
@@ -150,8 +156,11 @@ public:
     }
 
     // lib.rs:149-263 (prepare): one launch list per batch size, recorded as
-    // one graph; the down projection uses split-K slabs + reduce at batch 1
-    // (as the reference) or when selected, else the residual GEMM.
+    // one graph. The down projection uses split-K slabs + reduce at batch 1
+    // (as the reference) or when selected, else the residual GEMM. By
+    // default LayerNorm is folded into the QKV and gate/up GEMMs, fed by row
+    // statistics that the producers of x write (62 launches at b > 1); the
+    // unfused plan runs LayerNorm kernels as the reference does (86).
     void prepare(uint64_t b) {
         if (dhx_has_graph(engine_.get(), key(b))) return;
         const uint32_t r = (uint32_t)(b * tokens_);
@@ -167,38 +176,67 @@ public:
             l.push_back(x);
         };
         auto w = [&](const std::string& name) { return weights_.at(name); };
-        add(DHX_K_PATCH_EMBED, {B, G}, {region(kImage), w("patch_w"), w("patch_b"), w("prefix"), region(kX)});
-        add(DHX_K_LAYERNORM, {r}, {region(kX), w("l0_norm1_w"), w("l0_norm1_b"), region(kH)});
         const bool split = b == 1 || splitk_ == 1;
+        const dhx_region X = region(kX), H = region(kH), S = region(kStats);
+        if (fused_ln_) {
+            add(DHX_K_PATCH_EMBED_STATS, {B, G},
+                {region(kImage), w("patch_w"), w("patch_b"), w("prefix"), w("prefix_stats"), X, S});
+        } else {
+            add(DHX_K_PATCH_EMBED, {B, G}, {region(kImage), w("patch_w"), w("patch_b"), w("prefix"), X});
+            add(DHX_K_LAYERNORM, {r}, {X, w("l0_norm1_w"), w("l0_norm1_b"), H});
+        }
         for (int i = 0; i < 12; ++i) {
             const std::string p = "l" + std::to_string(i) + "_";
-            add(DHX_K_QKV_ROPE, {B, G, TP},
-                {region(kH), w(p + "qkv_w"), w(p + "qkv_b"), w("rope_cos"), w("rope_sin"), region(kQ), region(kK),
-                 region(kVt)});
+            const bool last = i == 11;
+            if (fused_ln_)
+                add(DHX_K_QKV_ROPE_LN, {B, G, TP},
+                    {X, S, w(p + "qkv_wln"), w(p + "qkv_wsum"), w(p + "qkv_t"), w("rope_cos"), w("rope_sin"),
+                     region(kQ), region(kK), region(kVt)});
+            else
+                add(DHX_K_QKV_ROPE, {B, G, TP},
+                    {H, w(p + "qkv_w"), w(p + "qkv_b"), w("rope_cos"), w("rope_sin"), region(kQ), region(kK),
+                     region(kVt)});
             add(DHX_K_ATTENTION, {B, G, TP}, {region(kQ), region(kK), region(kVt), region(kAttn)});
-            add(DHX_K_RESID, {r, 384}, {region(kAttn), w(p + "o_w"), w(p + "o_b"), w(p + "ls1"), region(kX)});
-            add(DHX_K_LAYERNORM, {r}, {region(kX), w(p + "norm2_w"), w(p + "norm2_b"), region(kH)});
-            add(DHX_K_SWIGLU, {r}, {region(kH), w(p + "gateup_w"), w(p + "gateup_b"), region(kAct)});
+            if (fused_ln_) {
+                add(DHX_K_RESID_STATS, {r, 384}, {region(kAttn), w(p + "o_w"), w(p + "o_b"), w(p + "ls1"), X, S});
+                add(DHX_K_SWIGLU_LN, {r},
+                    {X, S, w(p + "gateup_wln"), w(p + "gateup_wsum"), w(p + "gateup_t"), region(kAct)});
+            } else {
+                add(DHX_K_RESID, {r, 384}, {region(kAttn), w(p + "o_w"), w(p + "o_b"), w(p + "ls1"), X});
+                add(DHX_K_LAYERNORM, {r}, {X, w(p + "norm2_w"), w(p + "norm2_b"), H});
+                add(DHX_K_SWIGLU, {r}, {H, w(p + "gateup_w"), w(p + "gateup_b"), region(kAct)});
+            }
+            // The last block's statistics would have no reader (the final
+            // LayerNorm computes its own).
+            const bool stats = fused_ln_ && !last;
             if (split) {
                 add(DHX_K_SPLITK, {r, 1536, kSplits}, {region(kAct), w(p + "down_w"), region(kPartials)});
-                add(DHX_K_SPLITK_REDUCE, {r, kSplits}, {region(kPartials), w(p + "down_b"), w(p + "ls2"), region(kX)});
+                if (stats)
+                    add(DHX_K_SPLITK_REDUCE_STATS, {r, kSplits},
+                        {region(kPartials), w(p + "down_b"), w(p + "ls2"), X, S});
+                else
+                    add(DHX_K_SPLITK_REDUCE, {r, kSplits}, {region(kPartials), w(p + "down_b"), w(p + "ls2"), X});
+            } else if (stats) {
+                add(DHX_K_RESID_STATS, {r, 1536}, {region(kAct), w(p + "down_w"), w(p + "down_b"), w(p + "ls2"), X, S});
             } else {
-                add(DHX_K_RESID, {r, 1536}, {region(kAct), w(p + "down_w"), w(p + "down_b"), w(p + "ls2"), region(kX)});
+                add(DHX_K_RESID, {r, 1536}, {region(kAct), w(p + "down_w"), w(p + "down_b"), w(p + "ls2"), X});
             }
-            if (i < 11) {
+            if (!fused_ln_ && !last) {
                 const std::string n = "l" + std::to_string(i + 1) + "_";
-                add(DHX_K_LAYERNORM, {r}, {region(kX), w(n + "norm1_w"), w(n + "norm1_b"), region(kH)});
+                add(DHX_K_LAYERNORM, {r}, {X, w(n + "norm1_w"), w(n + "norm1_b"), H});
             }
         }
-        add(DHX_K_LAYERNORM_F32, {r}, {region(kX), w("norm_w"), w("norm_b"), region(kOut)});
+        add(DHX_K_LAYERNORM_F32, {r}, {X, w("norm_w"), w("norm_b"), region(kOut)});
         check(dhx_record(engine_.get(), key(b), l.data(), l.size()), engine_.get());
     }
 
-    // Graph key: batch size, plus a flag bit for the split-K variant.
-    uint64_t key(uint64_t b) const { return b | (splitk_ && b > 1 ? (1ull << 32) : 0); }
+    // Graph key: batch size plus one bit per plan variant.
+    uint64_t key(uint64_t b) const {
+        return b | (splitk_ && b > 1 ? (1ull << 32) : 0) | (fused_ln_ ? 0 : (1ull << 33));
+    }
 
 private:
-    enum { kX, kH, kQ, kK, kVt, kAttn, kAct, kOut, kImage, kPartials, kBuffers };
+    enum { kX, kH, kQ, kK, kVt, kAttn, kAct, kOut, kImage, kPartials, kStats, kBuffers };
     struct EngineFree {
         void operator()(dhx_engine* e) const { dhx_engine_free(e); }
     };
@@ -208,6 +246,7 @@ private:
     uint32_t size_ = 224, grid_ = 14;
     uint64_t patches_ = 196, tokens_ = 201, tpad_ = 256, image_elems_ = 0;
     int splitk_ = 0;
+    int fused_ln_ = 1;
     std::unique_ptr<dhx_engine, EngineFree> engine_;
     std::map<std::string, dhx_region> weights_;
     dhx_region a_[kBuffers];
@@ -352,6 +391,18 @@ int dinov3_replay(dinov3_model* m, uint64_t images) {
 
 int dinov3_set_splitk(dinov3_model* m, int mode) {
     return guarded(m, [&](dhx::Model& x) { x.set_splitk(mode); });
+}
+
+int dinov3_set_layernorm_fusion(dinov3_model* m, int on) {
+    return guarded(m, [&](dhx::Model& x) { x.set_layernorm_fusion(on); });
+}
+
+int dinov3_launch_timings(dinov3_model* m, uint64_t images, uint32_t iters, double* ms_out, uint32_t* kernel_out,
+                          uint64_t capacity, uint64_t* count) {
+    return guarded(m, [&](dhx::Model& x) {
+        if (dhx_launch_timings(x.engine(), x.key(images), iters, ms_out, kernel_out, capacity, count) != 0)
+            throw dhx::Error(dhx_last_error(x.engine()));
+    });
 }
 
 int dinov3_write_random_weights(const char* path, uint64_t seed, int preset) {

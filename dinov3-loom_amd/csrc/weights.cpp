@@ -67,6 +67,19 @@ std::vector<uint8_t> f32_bytes(const std::vector<float>& v) {
     return b;
 }
 
+// LayerNorm folded into the following GEMM: W' = f16(gamma[k] * W[n][k]),
+// wsum[n] = sum_k W'[n][k] (of the rounded values, so x.W'^T - mean*wsum is
+// exactly (x - mean).W'^T), t[n] = b[n] + sum_k beta[k] * W[n][k].
+struct Folded {
+    std::vector<uint8_t> w;
+    std::vector<float> wsum, t;
+};
+
+Folded fold_layernorm(const std::string& name, const std::vector<float>& w, const std::vector<float>& b,
+                      const std::vector<float>& gamma, const std::vector<float>& beta, size_t n, size_t k);
+
+std::vector<float> prefix_stats(const std::vector<float>& prefix);
+
 }  // namespace
 
 std::vector<uint8_t> pack_f16(const std::string& name, const float* values, size_t n) {
@@ -80,6 +93,49 @@ std::vector<uint8_t> pack_f16(const std::string& name, const float* values, size
     }
     return bytes;
 }
+
+namespace {
+
+Folded fold_layernorm(const std::string& name, const std::vector<float>& w, const std::vector<float>& b,
+                      const std::vector<float>& gamma, const std::vector<float>& beta, size_t n, size_t k) {
+    std::vector<float> scaled(n * k);
+    for (size_t r = 0; r < n; ++r)
+        for (size_t c = 0; c < k; ++c) scaled[r * k + c] = gamma[c] * w[r * k + c];
+    Folded f{pack_f16(name, scaled.data(), scaled.size()), std::vector<float>(n), std::vector<float>(n)};
+    for (size_t r = 0; r < n; ++r) {
+        double sum = 0.0, shift = b[r];
+        for (size_t c = 0; c < k; ++c) {
+            _Float16 h;
+            std::memcpy(&h, f.w.data() + 2 * (r * k + c), 2);
+            sum += (double)(float)h;
+            shift += (double)beta[c] * (double)w[r * k + c];
+        }
+        f.wsum[r] = (float)sum;
+        f.t[r] = (float)shift;
+    }
+    return f;
+}
+
+// Row statistics of the 5 prefix rows as stored in x (f16): per 64-column
+// slot, (mean, sum of squared deviations), laid out [row][slot][2].
+std::vector<float> prefix_stats(const std::vector<float>& prefix) {
+    std::vector<float> out(5 * 12);
+    for (int r = 0; r < 5; ++r)
+        for (int slot = 0; slot < 6; ++slot) {
+            double v[64], mean = 0.0, m2 = 0.0;
+            for (int c = 0; c < 64; ++c) {
+                v[c] = (double)(float)(_Float16)prefix[r * 384 + slot * 64 + c];
+                mean += v[c];
+            }
+            mean /= 64.0;
+            for (int c = 0; c < 64; ++c) m2 += (v[c] - mean) * (v[c] - mean);
+            out[r * 12 + slot * 2] = (float)mean;
+            out[r * 12 + slot * 2 + 1] = (float)m2;
+        }
+    return out;
+}
+
+}  // namespace
 
 Packed load_weights(const std::string& path, uint32_t grid) {
     const SafeTensors st(read_file(path));
@@ -95,6 +151,7 @@ Packed load_weights(const std::string& path, uint32_t grid) {
     const std::vector<float> reg = get(st, "embeddings.register_tokens", {1, 4, 384});
     prefix.insert(prefix.end(), reg.begin(), reg.end());
     emit("prefix", prefix, false);
+    emit("prefix_stats", prefix_stats(prefix), false);
     for (int i = 0; i < 12; ++i) {
         const std::string p = "layer." + std::to_string(i) + ".";
         const std::string l = "l" + std::to_string(i) + "_";
@@ -116,6 +173,13 @@ Packed load_weights(const std::string& path, uint32_t grid) {
         }
         emit(l + "qkv_w", qw, true);
         emit(l + "qkv_b", qb, false);
+        {
+            Folded f = fold_layernorm(l + "qkv_wln", qw, qb, get(st, p + "norm1.weight", {384}),
+                                      get(st, p + "norm1.bias", {384}), 1152, 384);
+            out.emplace_back(l + "qkv_wln", std::move(f.w));
+            emit(l + "qkv_wsum", f.wsum, false);
+            emit(l + "qkv_t", f.t, false);
+        }
         // Gate and up rows, interleaved in blocks of 32 so one wave's 64
         // GEMM columns are 32 gate outputs and the same 32 up outputs.
         const std::vector<float> gw = get(st, p + "mlp.gate_proj.weight", {1536, 384});
@@ -133,6 +197,13 @@ Packed load_weights(const std::string& path, uint32_t grid) {
             }
         emit(l + "gateup_w", w, true);
         emit(l + "gateup_b", b, false);
+        {
+            Folded f = fold_layernorm(l + "gateup_wln", w, b, get(st, p + "norm2.weight", {384}),
+                                      get(st, p + "norm2.bias", {384}), 3072, 384);
+            out.emplace_back(l + "gateup_wln", std::move(f.w));
+            emit(l + "gateup_wsum", f.wsum, false);
+            emit(l + "gateup_t", f.t, false);
+        }
         for (auto& v : {std::make_pair("o", std::make_pair("attention.o_proj", 384u)),
                         std::make_pair("down", std::make_pair("mlp.down_proj", 1536u))}) {
             emit(l + v.first + "_w", get(st, p + v.second.first + ".weight", {384, v.second.second}), true);

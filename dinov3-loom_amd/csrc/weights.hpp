@@ -16,10 +16,13 @@ using Packed = std::vector<std::pair<std::string, std::vector<uint8_t>>>;
 std::vector<uint8_t> pack_f16(const std::string& name, const float* values, size_t n);
 
 // weights.rs:19-146, with the RoPE tables built for a grid x grid patch grid.
-// Packed names: patch_w, patch_b, prefix, l{i}_{norm1_w, norm1_b, norm2_w,
-// norm2_b, ls1, ls2, qkv_w, qkv_b, gateup_w, gateup_b, o_w, o_b, down_w,
-// down_b}, norm_w, norm_b, rope_cos, rope_sin. gateup_w / gateup_b are
-// interleaved in blocks of 32 gate rows then the 32 matching up rows.
+// Packed names: patch_w, patch_b, prefix, prefix_stats, l{i}_{norm1_w,
+// norm1_b, norm2_w, norm2_b, ls1, ls2, qkv_w, qkv_b, qkv_wln, qkv_wsum,
+// qkv_t, gateup_w, gateup_b, gateup_wln, gateup_wsum, gateup_t, o_w, o_b,
+// down_w, down_b}, norm_w, norm_b, rope_cos, rope_sin. gateup_* rows are
+// interleaved in blocks of 32 gate rows then the 32 matching up rows. The
+// *_wln / *_wsum / *_t tensors fold the preceding LayerNorm into the GEMM
+// (see DHX_K_QKV_ROPE_LN in dinov3_engine.h).
 Packed load_weights(const std::string& path, uint32_t grid);
 
 void write_random_weights(const std::string& path, uint64_t seed, int preset);

@@ -32,7 +32,7 @@ FILE = "model.safetensors"
 
 # Kernel ids of include/dinov3_engine.h.
 KERNELS = ["patch_embed", "layernorm", "layernorm_f32", "qkv_rope", "attention", "resid", "swiglu", "splitk",
-           "splitk_reduce"]
+           "splitk_reduce", "patch_embed_stats", "qkv_rope_ln", "resid_stats", "swiglu_ln", "splitk_reduce_stats"]
 
 
 class DINOv3Error(RuntimeError):
@@ -56,10 +56,14 @@ class Region(ctypes.Structure):
     _fields_ = [("buffer", ctypes.c_uint32), ("offset", ctypes.c_uint64), ("bytes", ctypes.c_uint64)]
 
 
+MAX_SCALARS = 4  # DHX_MAX_SCALARS
+MAX_BINDINGS = 12  # DHX_MAX_BINDINGS
+
+
 class Launch(ctypes.Structure):
     """include/dinov3_engine.h dhx_launch (engine.rs:21-27 Launch)."""
-    _fields_ = [("kernel", ctypes.c_uint32), ("scalars", ctypes.c_uint32 * 4), ("n_bindings", ctypes.c_uint32),
-                ("bindings", Region * 8)]
+    _fields_ = [("kernel", ctypes.c_uint32), ("scalars", ctypes.c_uint32 * MAX_SCALARS),
+                ("n_bindings", ctypes.c_uint32), ("bindings", Region * MAX_BINDINGS)]
 
 
 def _load_library() -> ctypes.CDLL:
@@ -88,6 +92,9 @@ def _load_library() -> ctypes.CDLL:
     L.dinov3_stage.argtypes = [vp, fp, c.c_uint64]
     L.dinov3_replay.argtypes = [vp, c.c_uint64]
     L.dinov3_set_splitk.argtypes = [vp, c.c_int]
+    L.dinov3_set_layernorm_fusion.argtypes = [vp, c.c_int]
+    L.dinov3_launch_timings.argtypes = [vp, c.c_uint64, c.c_uint32, c.POINTER(c.c_double), c.POINTER(c.c_uint32),
+                                        c.c_uint64, c.POINTER(c.c_uint64)]
     L.dinov3_write_random_weights.argtypes = [c.c_char_p, c.c_uint64, c.c_int]
     L.dinov3_random_pixels.argtypes = [c.c_uint64, c.c_uint64, c.c_uint32, fp]
     L.dinov3_patchify.argtypes = [fp, c.c_uint64, c.c_uint32, fp]
@@ -255,18 +262,17 @@ class DINOv3:
         """0: residual GEMM for the down projection at batch > 1; 1: split-K + reduce."""
         _check(_lib.dinov3_set_splitk(self._h, int(mode)), self._h)
 
-    def graph_key(self, images: int, splitk: int = 0) -> int:
-        return int(images) | ((1 << 32) if splitk and images > 1 else 0)
+    def set_layernorm_fusion(self, on: bool) -> None:
+        """True (default): LayerNorm folded into the QKV / gate-up GEMMs; False: separate LayerNorm kernels."""
+        _check(_lib.dinov3_set_layernorm_fusion(self._h, int(bool(on))), self._h)
 
-    def launch_timings(self, images: int, iters: int = 20, splitk: int = 0) -> list[tuple[str, float]]:
-        """Average device ms of each launch of the recorded list (HIP events on the model's stream)."""
-        e = _lib.dinov3_engine(self._h)
+    def launch_timings(self, images: int, iters: int = 20) -> list[tuple[str, float]]:
+        """Average device ms of each launch of the plan recorded for `images` (HIP events on the model's stream)."""
         cap = 256
         ms = (ctypes.c_double * cap)()
         kid = (ctypes.c_uint32 * cap)()
         n = ctypes.c_uint64()
-        _check_engine(_lib.dhx_launch_timings(e, self.graph_key(images, splitk), int(iters), ms, kid, cap,
-                                              ctypes.byref(n)), e)
+        _check(_lib.dinov3_launch_timings(self._h, int(images), int(iters), ms, kid, cap, ctypes.byref(n)), self._h)
         return [(KERNELS[kid[i]], ms[i]) for i in range(n.value)]
 
     def _fail_next_gpu_call(self) -> None:
@@ -355,6 +361,8 @@ class Engine:
     def record(self, key: int, launches: list[tuple[int, list[int], list[Region]]]) -> None:
         arr = (Launch * len(launches))()
         for i, (kernel, scalars, bindings) in enumerate(launches):
+            if len(scalars) > MAX_SCALARS or len(bindings) > MAX_BINDINGS:
+                raise ValueError("too many scalars or bindings for one launch")
             arr[i].kernel = kernel
             for j, v in enumerate(scalars):
                 arr[i].scalars[j] = v

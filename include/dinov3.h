@@ -91,6 +91,15 @@ int dinov3_replay(dinov3_model *m, uint64_t images);
  * reduce (lib.rs:218-225; the reference's b = 1 path). Batch 1 always uses
  * split-K as in the reference. Graphs already recorded are dropped. */
 int dinov3_set_splitk(dinov3_model *m, int mode);
+/* LayerNorm plan (no reference counterpart): 1 (default) folds LayerNorm
+ * into the QKV and gate/up GEMMs from row statistics written by the kernels
+ * that produce the residual stream (62 launches per forward at b > 1);
+ * 0 runs separate LayerNorm kernels as the reference does (86 launches).
+ * Graphs are kept per (batch, variant). */
+int dinov3_set_layernorm_fusion(dinov3_model *m, int on);
+/* dhx_launch_timings for the plan the model would replay for `images`. */
+int dinov3_launch_timings(dinov3_model *m, uint64_t images, uint32_t iters, double *ms_out, uint32_t *kernel_out,
+                          uint64_t capacity, uint64_t *count);
 
 /* Seeded random-init weights (no reference counterpart): writes an
  * HF-named float32 safetensors file with every tensor the loader and the

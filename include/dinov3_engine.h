@@ -43,6 +43,20 @@ typedef struct dhx_region {
  *   DHX_K_SWIGLU        s = {rows}                   b = {h f16, gateup_w f16 [3072][384], gateup_b f32, act f16}
  *   DHX_K_SPLITK        s = {rows, k, splits}        b = {a f16, w f16 [384][k], partials f32 [splits][rows][384]}
  *   DHX_K_SPLITK_REDUCE s = {rows, splits}           b = {partials f32, b f32, ls f32, x f16}
+ *   DHX_K_PATCH_EMBED_STATS   s = {images, grid}   b = {pixels, patch_w, patch_b, prefix, prefix_stats f32 [5][12],
+ *                                                        x f16, stats f32 [rows][12]}
+ *   DHX_K_QKV_ROPE_LN         s = {images, grid, tpad}  b = {x f16, stats, qkv_wln f16 [1152][384], qkv_wsum f32,
+ *                                                        qkv_t f32, rope_cos, rope_sin, q, k, vt}
+ *   DHX_K_RESID_STATS         s = {rows, k}        b = {a, w, b, ls, x, stats}
+ *   DHX_K_SWIGLU_LN           s = {rows}           b = {x f16, stats, gateup_wln f16 [3072][384], gateup_wsum f32,
+ *                                                        gateup_t f32, act}
+ *   DHX_K_SPLITK_REDUCE_STATS s = {rows, splits}   b = {partials, b, ls, x, stats}
+ * The *_STATS kernels also write LayerNorm row statistics of the x they
+ * produce: stats[row][slot] = (mean, M2) of the f16 values of x in columns
+ * 64*slot .. 64*slot+63 (6 slots). The *_LN kernels apply LayerNorm to their
+ * input algebraically from those statistics: with W' = gamma (.) W (f16),
+ * wsum[n] = sum_k W'[n][k] and t = b + beta . W^T, out = rstd * (x . W'^T -
+ * mean * wsum) + t equals LN(x) . W^T + b.
  * q and k are [images][6][tpad][64] f16, vt is [images][6][64][tpad] f16,
  * tpad a multiple of 128 >= T = grid*grid + 5; k (and k / splits) a multiple
  * of 128 (the GEMM K loop runs stages of 64 in pairs). Every binding's size is
@@ -57,11 +71,16 @@ enum {
     DHX_K_SWIGLU = 6,
     DHX_K_SPLITK = 7,
     DHX_K_SPLITK_REDUCE = 8,
-    DHX_KERNEL_COUNT = 9
+    DHX_K_PATCH_EMBED_STATS = 9,
+    DHX_K_QKV_ROPE_LN = 10,
+    DHX_K_RESID_STATS = 11,
+    DHX_K_SWIGLU_LN = 12,
+    DHX_K_SPLITK_REDUCE_STATS = 13,
+    DHX_KERNEL_COUNT = 14
 };
 
 #define DHX_MAX_SCALARS 4
-#define DHX_MAX_BINDINGS 8
+#define DHX_MAX_BINDINGS 12
 
 /* One dispatch; replaces engine.rs:21-27 `Launch`. The grid is derived from
  * the scalars by each kernel's launcher. */

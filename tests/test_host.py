@@ -5,6 +5,7 @@ Hugging Face cache resolver. No test here launches GPU work."""
 import ctypes
 import os
 import re
+import subprocess
 
 import numpy as np
 import pytest
@@ -30,6 +31,24 @@ def test_library_exports_every_declared_function():
     assert len(names) > 30
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
+
+
+def test_binding_structs_match_header(tmp_path):
+    text = open(os.path.join(ROOT, "include", "dinov3_engine.h")).read()
+    consts = dict(re.findall(r"#define (DHX_MAX_\w+) (\d+)", text))
+    assert int(consts["DHX_MAX_SCALARS"]) == d.MAX_SCALARS and int(consts["DHX_MAX_BINDINGS"]) == d.MAX_BINDINGS
+    enum = dict((n, int(v)) for n, v in re.findall(r"(DHX_K_\w+) = (\d+)", text))
+    assert [n[6:].lower() for n, _ in sorted(enum.items(), key=lambda kv: kv[1])] == d.KERNELS
+    # the struct layouts the C compiler gives the header
+    src = tmp_path / "layout.c"
+    src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "dinov3.h"\nint main(void) {'
+                   'printf("%zu %zu %zu %zu %zu\\n", sizeof(dhx_region), sizeof(dhx_launch), '
+                   'offsetof(dhx_launch, bindings), sizeof(dinov3_options), sizeof(dhx_timings)); return 0; }\n')
+    exe = tmp_path / "layout"
+    subprocess.check_call(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)])
+    sizes = [int(v) for v in subprocess.check_output([str(exe)]).split()]
+    assert sizes == [ctypes.sizeof(d.Region), ctypes.sizeof(d.Launch), d.Launch.bindings.offset,
+                     ctypes.sizeof(d._Options), ctypes.sizeof(d._Timings)]
 
 
 def test_constants_match_reference():

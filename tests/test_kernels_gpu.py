@@ -18,7 +18,8 @@ from conftest import cosine
 
 pytestmark = pytest.mark.gpu
 
-K_PATCH, K_LN, K_LN32, K_QKV, K_ATTN, K_RESID, K_SWIGLU, K_SPLITK, K_REDUCE = range(9)
+(K_PATCH, K_LN, K_LN32, K_QKV, K_ATTN, K_RESID, K_SWIGLU, K_SPLITK, K_REDUCE, K_PATCH_S, K_QKV_LN, K_RESID_S,
+ K_SWIGLU_LN, K_REDUCE_S) = range(14)
 _keys = iter(range(1000, 100000))
 
 
@@ -253,3 +254,125 @@ def test_launch_validation_happens_before_any_launch(eng):
         eng.record(next(_keys), [(K_ATTN, [1, 14, 200], [big, big, big, big])])
     with pytest.raises(d.DINOv3Error, match="not been prepared"):
         eng.replay(987654321)
+
+
+# ---------------------------------------------------------------------------
+# LayerNorm fused through row statistics (DHX_K_*_STATS producers and
+# DHX_K_*_LN consumers).
+
+def slot_stats(x):
+    """(mean, M2) of each 64-column slot of each row, float64 -> [rows, 12] f32."""
+    v = np.asarray(x, np.float64).reshape(-1, 6, 64)
+    mean = v.mean(2)
+    m2 = ((v - mean[..., None]) ** 2).sum(2)
+    return np.stack([mean, m2], 2).reshape(-1, 12).astype(np.float32)
+
+
+def check_stats(gpu_stats, x_f16, what):
+    want = slot_stats(x_f16)
+    got = np.asarray(gpu_stats, np.float64).reshape(-1, 12)
+    mean_err = np.abs(got[:, 0::2] - want[:, 0::2]).max()
+    m2_rel = (np.abs(got[:, 1::2] - want[:, 1::2]) / (want[:, 1::2] + 1e-6)).max()
+    print(f"{what}: stats mean err {mean_err:.3g}, M2 rel err {m2_rel:.3g}")
+    assert mean_err < 1e-5 * (1 + np.abs(want[:, 0::2]).max()) and m2_rel < 1e-4
+
+
+def fold(w, b, gamma, beta):
+    """LayerNorm folded into a GEMM: W' = f16(gamma*W), wsum = sum_k W', t = b + beta.W^T."""
+    wl = f16(gamma[None, :].astype(np.float32) * w.astype(np.float32))
+    return wl, wl.astype(np.float64).sum(1).astype(np.float32), (b + beta.astype(np.float64) @ w.T.astype(np.float64)).astype(np.float32)
+
+
+@pytest.mark.parametrize("rows,kdim", [(1001, 384), (12864, 1536)])
+def test_resid_stats(eng, rows, kdim):
+    rng = np.random.default_rng(rows + 3 * kdim)
+    a = f16(rng.normal(size=(rows, kdim)))
+    w = f16(rng.normal(size=(384, kdim)) * 0.03)
+    b = (rng.normal(size=384) * 0.1).astype(np.float32)
+    ls = rng.uniform(0.5, 1.5, size=384).astype(np.float32)
+    x0 = f16(rng.normal(size=(rows, 384)) * 2 + 0.7)
+    x, st = up(eng, x0), eng.allocate(rows * 48)
+    run(eng, K_RESID_S, [rows, kdim], [up(eng, a), up(eng, w), up(eng, b), up(eng, ls), x, st])
+    y = eng.read(x, np.float16, (rows, 384))
+    ref = x0.astype(np.float64) + ls * oracle.linear(a.astype(np.float64), w.astype(np.float64), b)
+    check(y, ref, atol=2e-3, what=f"resid+stats rows={rows} k={kdim}")
+    check_stats(eng.read(st, np.float32, (rows, 12)), y, "resid stats")
+
+
+@pytest.mark.parametrize("rows", [201, 1001])
+def test_splitk_reduce_stats(eng, rows):
+    rng = np.random.default_rng(rows + 11)
+    part = (rng.normal(size=(4, rows, 384)) * 0.5).astype(np.float32)
+    b = (rng.normal(size=384) * 0.1).astype(np.float32)
+    ls = rng.uniform(0.5, 1.5, size=384).astype(np.float32)
+    x0 = f16(rng.normal(size=(rows, 384)))
+    x, st = up(eng, x0), eng.allocate(rows * 48)
+    run(eng, K_REDUCE_S, [rows, 4], [up(eng, part), up(eng, b), up(eng, ls), x, st])
+    y = eng.read(x, np.float16, (rows, 384))
+    ref = x0.astype(np.float64) + ls * (part.astype(np.float64).sum(0) + b)
+    check(y, ref, atol=2e-3, what="reduce+stats")
+    check_stats(eng.read(st, np.float32, (rows, 12)), y, "reduce stats")
+
+
+@pytest.mark.parametrize("images,grid", [(3, 14), (1, 32)])
+def test_patch_embed_stats(eng, images, grid):
+    rng = np.random.default_rng(images + grid)
+    S, T = 16 * grid, grid * grid + 5
+    px = rng.normal(size=(images, 3, S, S)).astype(np.float32)
+    w = f16(rng.normal(size=(384, 768)) * 0.02)
+    b = (rng.normal(size=384) * 0.1).astype(np.float32)
+    prefix = rng.normal(size=(5, 384)).astype(np.float32)
+    pstats = slot_stats(f16(prefix))
+    x, st = eng.allocate(images * T * 768), eng.allocate(images * T * 48)
+    run(eng, K_PATCH_S, [images, grid], [up(eng, px), up(eng, w), up(eng, b), up(eng, prefix), up(eng, pstats), x, st])
+    y = eng.read(x, np.float16, (images, T, 384))
+    a = oracle.round_f16(oracle.patchify(px, grid))
+    ref = oracle.linear(a, w.astype(np.float64), b).reshape(images, grid * grid, 384)
+    check(y[:, 5:], ref, atol=2e-4, what="patch embed (stats variant)")
+    check_stats(eng.read(st, np.float32, (images * T, 12)), y.reshape(-1, 384), "patch stats")
+
+
+@pytest.mark.parametrize("images,grid,offset", [(3, 14, 0.0), (1, 32, 0.5), (2, 14, 4.0)])
+def test_qkv_rope_layernorm_fused(eng, images, grid, offset):
+    rng = np.random.default_rng(grid * 7 + int(offset * 10))
+    T = grid * grid + 5
+    tpad = (T + 127) // 128 * 128
+    x = f16(rng.normal(size=(images * T, 384)) * 1.5 + offset)
+    gamma = (1 + rng.normal(size=384) * 0.2).astype(np.float32)
+    beta = (rng.normal(size=384) * 0.2).astype(np.float32)
+    w = (rng.normal(size=(1152, 384)) * 0.05).astype(np.float32)
+    b = (rng.normal(size=1152) * 0.1).astype(np.float32)
+    wl, wsum, t = fold(w, b, gamma, beta)
+    cos, sin = oracle.rope_tables(grid)
+    nb = images * 6 * tpad * 64 * 2
+    q, k, vt = eng.allocate(nb), eng.allocate(nb), eng.allocate(nb)
+    run(eng, K_QKV_LN, [images, grid, tpad],
+        [up(eng, x), up(eng, slot_stats(x)), up(eng, wl), up(eng, wsum), up(eng, t), up(eng, cos), up(eng, sin),
+         q, k, vt])
+    gq = eng.read(q, np.float16, (images, 6, tpad, 64))
+    gv = eng.read(vt, np.float16, (images, 6, 64, tpad))
+    h = oracle.layernorm(x.astype(np.float64), gamma, beta)  # LN(x), unrounded
+    for i in range(images):
+        rows = h[i * T:(i + 1) * T]
+        rq = oracle.rope(oracle.linear(rows, w[:384].astype(np.float64), b[:384]), grid)
+        rv = oracle.linear(rows, w[768:].astype(np.float64), b[768:])
+        check(gq[i, :, :T].transpose(1, 0, 2).reshape(T, 384), rq, atol=3e-3, what=f"fused-LN q img {i}")
+        check(gv[i, :, :, :T].transpose(2, 0, 1).reshape(T, 384), rv, atol=3e-3, what=f"fused-LN v img {i}")
+
+
+@pytest.mark.parametrize("rows,offset", [(1001, 0.0), (12864, 2.0)])
+def test_swiglu_layernorm_fused(eng, rows, offset):
+    rng = np.random.default_rng(rows + 17)
+    x = f16(rng.normal(size=(rows, 384)) + offset)
+    gamma = (1 + rng.normal(size=384) * 0.2).astype(np.float32)
+    beta = (rng.normal(size=384) * 0.2).astype(np.float32)
+    wg, wu = (rng.normal(size=(1536, 384)) * 0.05).astype(np.float32), (rng.normal(size=(1536, 384)) * 0.05).astype(np.float32)
+    bg, bu = (rng.normal(size=1536) * 0.2).astype(np.float32), (rng.normal(size=1536) * 0.2).astype(np.float32)
+    w, b = pack_gateup(wg, wu, bg, bu)
+    wl, wsum, t = fold(w, b, gamma, beta)
+    act = eng.allocate(rows * 1536 * 2)
+    run(eng, K_SWIGLU_LN, [rows], [up(eng, x), up(eng, slot_stats(x)), up(eng, wl), up(eng, wsum), up(eng, t), act])
+    y = eng.read(act, np.float16, (rows, 1536))
+    h = oracle.layernorm(x.astype(np.float64), gamma, beta)
+    ref = oracle.swiglu(oracle.linear(h, wg.astype(np.float64), bg), oracle.linear(h, wu.astype(np.float64), bu))
+    check(y, ref, atol=3e-3, what=f"fused-LN swiglu rows={rows}")

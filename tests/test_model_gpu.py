@@ -115,6 +115,24 @@ def test_full_batch_64_rows_independent_of_batch(models, oracle_weights):
         assert c_all > 0.9999 and c_cls > 0.9999
 
 
+@pytest.mark.parametrize("preset", [0, 1])
+def test_layernorm_fusion_matches_unfused_plan(models, oracle_weights, preset):
+    m = models(preset, max_batch=8)
+    px = d.random_pixels(6, 8)
+    fused = m.forward(px)
+    m.set_layernorm_fusion(False)
+    try:
+        plain = m.forward(px)
+    finally:
+        m.set_layernorm_fusion(True)
+    for i in range(8):
+        assert cosine(fused[i], plain[i]) > 0.99999
+    want = oracle.forward(oracle_weights(preset), px[0], 14)
+    c_all, c_cls, _ = compare(plain[0], want, f"unfused plan preset {preset}")
+    assert c_all > 0.9999 and c_cls > 0.9999
+    compare(fused[0], want, f"fused plan preset {preset}")
+
+
 def test_splitk_variant(models):
     m = models(1, max_batch=8)
     px = d.random_pixels(5, 8)
