@@ -292,8 +292,12 @@ int dhx_allocate(dhx_engine* e, uint64_t bytes, dhx_region* out) {
         hip_check(e, hipMalloc(&p, std::max<uint64_t>(bytes, 16)), "hipMalloc");
         e->buffers.push_back(p);
         e->sizes.push_back(bytes);
-        // Zero once: padded rows of q/k/v^T are never written and must stay finite.
-        hip_check(e, hipMemset(p, 0, std::max<uint64_t>(bytes, 16)), "hipMemset");
+        // Zero once: padded rows of q/k/v are never written and must stay finite.
+        // The engine's stream does not synchronise with the legacy default
+        // stream, so the fill is queued on it and waited for: a later upload or
+        // kernel on that stream can never overtake it.
+        hip_check(e, hipMemsetAsync(p, 0, std::max<uint64_t>(bytes, 16), e->stream), "hipMemsetAsync");
+        hip_check(e, hipStreamSynchronize(e->stream), "allocation synchronize");
         *out = dhx_region{(uint32_t)(e->buffers.size() - 1), 0, bytes};
     });
 }
@@ -301,7 +305,8 @@ int dhx_allocate(dhx_engine* e, uint64_t bytes, dhx_region* out) {
 int dhx_weight(dhx_engine* e, const void* bytes, uint64_t n, dhx_region* out) {
     return guarded(e, [&] {
         if (dhx_allocate(e, n, out) != 0) throw dhx::Error(e->error);
-        hip_check(e, hipMemcpy(region_ptr(e, *out), bytes, n, hipMemcpyHostToDevice), "weight upload");
+        hip_check(e, hipMemcpyAsync(region_ptr(e, *out), bytes, n, hipMemcpyHostToDevice, e->stream), "weight upload");
+        hip_check(e, hipStreamSynchronize(e->stream), "weight upload synchronize");
     });
 }
 

@@ -2,13 +2,14 @@
 // kernels/attention_online_f16_wmma_cf16.loom).
 //
 // One workgroup = 4 waves = 128 queries of one (image, head); each wave owns
-// 32 queries. Keys stream through LDS in blocks of 64 (K as [key][ch], V
-// transposed as [ch][key], both double-buffered), so the same kernel serves
-// 201 tokens (224x224) and 1029 tokens (512x512).
+// 32 queries. Keys stream through LDS in blocks of 64 (K and V both as
+// [key][ch], double-buffered), so the same kernel serves 201 tokens
+// (224x224) and 1029 tokens (512x512).
 //
 // Everything is computed transposed so that a lane owns one query:
 //   S^T = K . Q^T      (MFMA a = K rows from LDS, b = Q^T held in registers)
-//   O^T += V^T . P^T   (MFMA a = V^T rows from LDS, b = P^T straight from the
+//   O^T += V^T . P^T   (MFMA a = V^T rows, read out of the [key][ch] V block
+//                       with LDS transpose reads; b = P^T straight from the
 //                       S^T accumulators)
 // Lane l holds query (l % 32) and 16 of every 32 keys; the other 16 are in
 // lane l ^ 32, so each row max / row sum is 15 in-register ops plus one
@@ -33,7 +34,7 @@ __device__ __forceinline__ half8_t zero8() {
 
 __global__ __launch_bounds__(kThreads) void attention_kernel(AttentionArgs p) {
     __shared__ half_t sK[2][KB * KLD];
-    __shared__ half_t sV[2][kHeadDim * KLD];
+    __shared__ half_t sV[2][KB * KLD];
     // 1-D grid, XCD-aware: the tile space (query block fastest, then head,
     // then image) is cut into 8 contiguous chunks, one per XCD, so the query
     // blocks of one (image, head) share K and V in that XCD's L2.
@@ -47,7 +48,7 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttentionArgs p) {
     const size_t bh = (size_t)img * kHeads + head;
     const half_t* qg = p.q + bh * p.tpad * kHeadDim;
     const half_t* kg = p.k + bh * p.tpad * kHeadDim;
-    const half_t* vg = p.vt + bh * kHeadDim * p.tpad;
+    const half_t* vg = p.v + bh * p.tpad * kHeadDim;
 
     const int qrow = qb * QB + wave * 32 + l32;
     half8_t qf[4];
@@ -55,14 +56,14 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttentionArgs p) {
     for (int kk = 0; kk < 4; ++kk)
         qf[kk] = qrow < T ? *(const half8_t*)(qg + (size_t)qrow * kHeadDim + kk * 16 + hi * 8) : zero8();
 
-    // Each thread moves two 16-byte pieces of the K block and two of V^T.
+    // Each thread moves two 16-byte pieces of the K block and two of V.
     half8_t kr[2], vr[2];
     auto load = [&](int kb) {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int c = tid + i * kThreads, row = c >> 3, col = (c & 7) * 8;
             kr[i] = *(const half8_t*)(kg + (size_t)(kb * KB + row) * kHeadDim + col);
-            vr[i] = *(const half8_t*)(vg + (size_t)row * p.tpad + kb * KB + col);
+            vr[i] = *(const half8_t*)(vg + (size_t)(kb * KB + row) * kHeadDim + col);
         }
     };
     auto store = [&](int buf) {
@@ -73,6 +74,11 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttentionArgs p) {
             *(half8_t*)(&sV[buf][row * KLD + col]) = vr[i];
         }
     };
+
+    // Transpose-read position of this lane inside a 4-key x 32-channel patch
+    // of the V block: lane j of each 16-lane group then receives channel
+    // 16*(group%2) + j of four consecutive keys.
+    const int tr_row = (lane & 15) >> 2, tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
     const float scale = 0.125f * kLog2e;
     const float neg_inf = -__builtin_inff();
@@ -118,8 +124,8 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttentionArgs p) {
             o[0] *= alpha;
             o[1] *= alpha;
             // P^T as the b operand: k-slice element j of this lane is key
-            // key0 + 16ks + (j < 4 ? 4hi + j : 8 + 4hi + j - 4); the V^T reads
-            // below pick the same keys.
+            // key0 + 16ks + (j < 4 ? 4hi + j : 8 + 4hi + j - 4); the V^T
+            // transpose reads below give channel ct*32 + l32 of the same keys.
             half8_t pb[2];
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks)
@@ -129,8 +135,8 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttentionArgs p) {
             for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
                 for (int ks = 0; ks < 2; ++ks) {
-                    const half_t* vrow = &sV[buf][(ct * 32 + l32) * KLD + sub * 32 + ks * 16 + 4 * hi];
-                    const half4_t a0 = *(const half4_t*)vrow, a1 = *(const half4_t*)(vrow + 8);
+                    const half_t* vb = &sV[buf][(sub * 32 + ks * 16 + 4 * hi + tr_row) * KLD + ct * 32 + tr_col];
+                    const half4_t a0 = lds_read_tr16(vb), a1 = lds_read_tr16(vb + 8 * KLD);
                     const half8_t va = __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7);
                     o[ct] = mfma32x32x16(va, pb[ks], o[ct]);
                 }

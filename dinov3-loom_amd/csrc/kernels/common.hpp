@@ -30,6 +30,24 @@ __device__ __forceinline__ float16_t mfma32x32x16(half8_t a, half8_t b, float16_
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+typedef short short4_t __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16 (gfx950 LDS transpose read). Within each group of 16
+// lanes, lane j receives element j % 4 of the 8-byte words addressed by lanes
+// j/4, j/4 + 4, j/4 + 8 and j/4 + 12, in that order. If lane i of the group
+// addresses row r0 + i/4, columns c0 + 4*(i%4) .. +3 of a row-major f16
+// matrix, lane j gets column c0 + j of rows r0 .. r0+3. p must be 8-byte
+// aligned and point into LDS.
+__device__ __forceinline__ half4_t lds_read_tr16(const half_t* p) {
+    const short4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_t*)p);
+    return __builtin_bit_cast(half4_t, v);
+}
+
+// Orders this wave's earlier LDS writes before its later LDS reads (of words
+// other lanes wrote): a wave's LDS instructions complete in issue order, and
+// the clobber keeps the compiler from moving LDS accesses across this point.
+__device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);

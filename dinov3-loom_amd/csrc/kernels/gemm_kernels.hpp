@@ -45,35 +45,35 @@ struct PatchRows {
     }
 };
 
-// Writes this wave's (mean, M2) partial of row m over its 64 columns: the
-// lane holds 32 of them (v, already rounded to the f16 values stored in x),
-// its partner lane l ^ 32 the other 32. Both partners must call this.
-__device__ __forceinline__ void slot_stats(float* stats, size_t m, int slot, const float4_t (&v)[2][4], int hi) {
-    float s = 0.f;
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) s += (v[i][g][0] + v[i][g][1]) + (v[i][g][2] + v[i][g][3]);
-    s += __shfl_xor(s, 32, 64);
+// Writes the (mean, M2) partial of row m over the 64 columns of one
+// statistics slot, whose values are spread over 8 consecutive lanes (8 each,
+// already rounded to the f16 values stored in x). All 8 lanes must call this.
+__device__ __forceinline__ void slot_stats(float* stats, size_t m, int slot, const float (&v)[8], int lane8) {
+    float s = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    s += __shfl_xor(s, 4, 64);
     const float mean = s * (1.0f / 64.0f);
     float q = 0.f;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int g = 0; g < 4; ++g)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) q += (v[i][g][e] - mean) * (v[i][g][e] - mean);
-    q += __shfl_xor(q, 32, 64);
-    if (hi == 0) *(float2_t*)(stats + m * kStatFloats + slot * 2) = float2_t{mean, q};
+    for (int e = 0; e < 8; ++e) q += (v[e] - mean) * (v[e] - mean);
+    q += __shfl_xor(q, 1, 64);
+    q += __shfl_xor(q, 2, 64);
+    q += __shfl_xor(q, 4, 64);
+    if (lane8 == 0) *(float2_t*)(stats + m * kStatFloats + slot * 2) = float2_t{mean, q};
 }
 
 __device__ __forceinline__ float4_t widen(half4_t h) { return float4_t{(float)h[0], (float)h[1], (float)h[2], (float)h[3]}; }
 
 // Patch embedding + CLS/register scatter into the f16 residual stream x
-// (with STATS, also the LayerNorm row statistics of x).
+// (with STATS, also the LayerNorm row statistics of x). Each wave rounds its
+// 32 x 64 block to f16 into LDS, then writes it as 128-byte row pieces
+// (8 lanes per row), which is also the layout the row statistics need.
 template <class T, bool STATS>
 __global__ __launch_bounds__(T::THREADS) void patch_embed_kernel(PatchEmbedArgs p) {
-    static_assert(!STATS || T::TN == 64, "one statistics slot per wave");
+    static_assert(T::TN == 64, "one statistics slot per wave");
+    constexpr int SP = T::TN + 8;  // staging pitch in halfs
+    static_assert(T::WAVES * T::TM * SP <= T::LDS_HALFS, "staging fits the stage buffers");
     __shared__ __attribute__((aligned(16))) half_t lds[T::LDS_HALFS];
     const int P = p.grid * p.grid, Tok = P + kPrefix, M = p.images * P;
     constexpr int NT = kHidden / T::BN;
@@ -82,24 +82,32 @@ __global__ __launch_bounds__(T::THREADS) void patch_embed_kernel(PatchEmbedArgs 
     WeightRows<T> wl[2] = {{{}, p.w, 768, 0}, {{}, p.w, 768, 0}};
     gemm_tile<T>(al, wl, NT, NT * ((M + T::BM - 1) / T::BM), 768 / BK, lds, [&](const Acc<T>& acc, int m0, int n0) {
         const Frag<T> f(m0, n0);
+        half_t* const st = lds + (threadIdx.x >> 6) * (T::TM * SP);
 #pragma unroll
-        for (int j = 0; j < T::FM; ++j) {
-            const int m = f.row(j);
-            if (m >= M) continue;
-            const int img = m / P, patch = m - img * P;
-            const size_t row = (size_t)img * Tok + kPrefix + patch;
-            half_t* dst = p.x + row * kHidden;
-            float4_t v[T::FN][4];
+        for (int i = 0; i < T::FN; ++i)
 #pragma unroll
-            for (int i = 0; i < T::FN; ++i)
+            for (int g = 0; g < 4; ++g) {
+                const int n = f.col(i, g);
+                const float4_t b = ld4(p.bias + n);
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const int n = f.col(i, g);
-                    const half4_t h = to_half4(group4(acc.v[i][j], g) + ld4(p.bias + n));
-                    *(half4_t*)(dst + n) = h;
-                    v[i][g] = widen(h);
-                }
-            if constexpr (STATS) slot_stats(p.stats, row, f.n_base / 64, v, f.hi);
+                for (int j = 0; j < T::FM; ++j)
+                    *(half4_t*)(st + (j * 32 + f.l32) * SP + (n - f.n_base)) = to_half4(group4(acc.v[i][j], g) + b);
+            }
+        wave_lds_sync();
+        const int lane = threadIdx.x & 63, r0 = lane >> 3, c8 = (lane & 7) * 8;
+#pragma unroll
+        for (int it = 0; it < T::TM / 8; ++it) {
+            const int r = it * 8 + r0, m = f.m_base + r;
+            if (m >= M) continue;  // uniform over the 8 lanes of a row
+            const size_t row = (size_t)m + (size_t)(m / P + 1) * kPrefix;  // image*Tok + kPrefix + patch
+            const half8_t h = *(const half8_t*)(st + r * SP + c8);
+            *(half8_t*)(p.x + row * kHidden + f.n_base + c8) = h;
+            if constexpr (STATS) {
+                float v[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = (float)h[e];
+                slot_stats(p.stats, row, f.n_base / 64, v, lane & 7);
+            }
         }
         // CLS + registers of every image whose first patch row lies in this tile.
         const int m_end = min(m0 + T::BM, M);
@@ -122,10 +130,17 @@ __global__ __launch_bounds__(T::THREADS) void patch_embed_kernel(PatchEmbedArgs 
 
 // QKV + bias + 2D RoPE. A wave's 64 columns are exactly one head of q, k or
 // v, so channel c and its rotation partner c+32 are acc.v[0] / acc.v[1] of
-// the same lane. q, k are written head-major, v transposed.
+// the same lane, and both use angle column c of the RoPE tables (DINOv3's
+// tables repeat columns 0..31 in 32..63; only the first half is read).
+// Results are rounded to f16 into a per-wave LDS block, then each wave
+// writes its rows as whole 128-byte head rows: q, k and v are all
+// head-major [image][head][tpad][64], and the rows of one image are
+// contiguous there.
 template <class T, bool LN>
 __global__ __launch_bounds__(T::THREADS) void qkv_rope_kernel(QkvArgs p) {
     static_assert(T::TN == kHeadDim, "one head per wave");
+    constexpr int SP = kHeadDim + 8;  // staging pitch in halfs
+    static_assert(T::WAVES * T::TM * SP <= T::LDS_HALFS, "staging fits the stage buffers");
     __shared__ __attribute__((aligned(16))) half_t lds[T::LDS_HALFS];
     const int P = p.grid * p.grid, Tok = P + kPrefix, M = p.images * Tok;
     constexpr int NT = 3 * kHidden / T::BN;
@@ -133,56 +148,79 @@ __global__ __launch_bounds__(T::THREADS) void qkv_rope_kernel(QkvArgs p) {
     WeightRows<T> wl[2] = {{{}, p.w, kHidden, 0}, {{}, p.w, kHidden, 0}};
     gemm_tile<T>(al, wl, NT, NT * ((M + T::BM - 1) / T::BM), kHidden / BK, lds, [&](const Acc<T>& acc, int m0, int n0) {
         const Frag<T> f(m0, n0);
+        const int lane = threadIdx.x & 63;
+        half_t* const st = lds + (threadIdx.x >> 6) * (T::TM * SP);
         const int part = f.n_base / kHidden, head = (f.n_base % kHidden) / kHeadDim;
+        float4_t bias[2][4], wsum[2][4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int c = g * 8 + f.hi * 4;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                bias[i][g] = ld4(p.bias + f.n_base + 32 * i + c);
+                if constexpr (LN) wsum[i][g] = ld4(p.wsum + f.n_base + 32 * i + c);
+            }
+        }
 #pragma unroll
         for (int j = 0; j < T::FM; ++j) {
-            const int m = f.row(j);
-            if (m >= M) continue;
-            const int img = m / Tok, tok = m - img * Tok;
-            const size_t bh = (size_t)img * kHeads + head;
+            const int m = min(f.row(j), M - 1);  // rows past M are computed but never written out
+            const int tok = m % Tok;
             const bool rotate = part < 2 && tok >= kPrefix;
+            const size_t angle_row = (size_t)max(tok - kPrefix, 0) * kHeadDim;
             RowNorm rn{0.f, 1.f};
             if constexpr (LN) rn = row_norm(p.stats, m);
+            half_t* const row = st + (j * 32 + f.l32) * SP;
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int c = g * 8 + f.hi * 4;  // channel in the head (0..31); partner c + 32
                 float4_t lo = group4(acc.v[0][j], g), up = group4(acc.v[1][j], g);
                 if constexpr (LN) {
-                    lo = (lo - rn.mean * ld4(p.wsum + f.n_base + c)) * rn.rstd;
-                    up = (up - rn.mean * ld4(p.wsum + f.n_base + 32 + c)) * rn.rstd;
+                    lo = (lo - rn.mean * wsum[0][g]) * rn.rstd;
+                    up = (up - rn.mean * wsum[1][g]) * rn.rstd;
                 }
-                lo += ld4(p.bias + f.n_base + c);
-                up += ld4(p.bias + f.n_base + 32 + c);
+                lo += bias[0][g];
+                up += bias[1][g];
                 if (rotate) {
-                    const float* cs = p.cos + (tok - kPrefix) * kHeadDim;
-                    const float* sn = p.sin + (tok - kPrefix) * kHeadDim;
-                    const float4_t nlo = lo * ld4(cs + c) - up * ld4(sn + c);            // x[c]cos - x[c+32]sin
-                    const float4_t nup = up * ld4(cs + 32 + c) + lo * ld4(sn + 32 + c);  // x[c+32]cos + x[c]sin
+                    const float4_t co = ld4(p.cos + angle_row + c), si = ld4(p.sin + angle_row + c);
+                    const float4_t nlo = lo * co - up * si;  // x[c] cos - x[c+32] sin
+                    const float4_t nup = up * co + lo * si;  // x[c+32] cos + x[c] sin
                     lo = nlo;
                     up = nup;
                 }
-                if (part < 2) {
-                    half_t* dst = (part == 0 ? p.q : p.k) + (bh * p.tpad + tok) * kHeadDim;
-                    *(half4_t*)(dst + c) = to_half4(lo);
-                    *(half4_t*)(dst + 32 + c) = to_half4(up);
-                } else {
-                    half_t* dst = p.vt + bh * kHeadDim * p.tpad + tok;
+                *(half4_t*)(row + c) = to_half4(lo);
+                *(half4_t*)(row + 32 + c) = to_half4(up);
+            }
+        }
+        wave_lds_sync();
+        // Copy-out: 8 lanes per 128-byte row, 8 rows per pass.
+        half_t* const out = part == 0 ? p.q : part == 1 ? p.k : p.v;
+        const int r0 = lane >> 3, ch = (lane & 7) * 8;
+        int m = f.m_base + r0;
+        int img = m / Tok, tok = m - img * Tok;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        dst[(size_t)(c + e) * p.tpad] = (half_t)lo[e];
-                        dst[(size_t)(c + 32 + e) * p.tpad] = (half_t)up[e];
-                    }
-                }
+        for (int it = 0; it < T::TM / 8; ++it) {
+            if (m < M)
+                *(half8_t*)(out + (((size_t)img * kHeads + head) * p.tpad + tok) * kHeadDim + ch) =
+                    *(const half8_t*)(st + (it * 8 + r0) * SP + ch);
+            m += 8;
+            tok += 8;
+            while (tok >= Tok) {
+                tok -= Tok;
+                ++img;
             }
         }
     });
 }
 
 // Residual GEMM: x += ls * (A W^T + b), in place on the f16 residual stream
-// (with STATS, also the LayerNorm row statistics of the updated x).
+// (with STATS, also the LayerNorm row statistics of the updated x). Each wave
+// stages its f32 update (32 x 64) in LDS, then reads and writes x as
+// 128-byte row pieces, 8 lanes per row.
 template <class T, bool STATS>
 __global__ __launch_bounds__(T::THREADS) void resid_kernel(ResidArgs p) {
-    static_assert(!STATS || T::TN == 64, "one statistics slot per wave");
+    static_assert(T::TN == 64, "one statistics slot per wave");
+    constexpr int SPF = T::TN + 4;  // staging pitch in floats
+    static_assert(T::WAVES * T::TM * SPF * 4 <= T::LDS_BYTES, "staging fits the stage buffers");
     __shared__ __attribute__((aligned(16))) half_t lds[T::LDS_HALFS];
     constexpr int NT = kHidden / T::BN;
     ActRows<T> al[2] = {{{}, p.a, p.k, p.rows, 0}, {{}, p.a, p.k, p.rows, 0}};
@@ -190,33 +228,54 @@ __global__ __launch_bounds__(T::THREADS) void resid_kernel(ResidArgs p) {
     gemm_tile<T>(al, wl, NT, NT * ((p.rows + T::BM - 1) / T::BM), p.k / BK, lds,
                        [&](const Acc<T>& acc, int m0, int n0) {
         const Frag<T> f(m0, n0);
+        float* const st = reinterpret_cast<float*>(lds) + (threadIdx.x >> 6) * (T::TM * SPF);
 #pragma unroll
-        for (int j = 0; j < T::FM; ++j) {
-            const int m = f.row(j);
-            if (m >= p.rows) continue;
-            half_t* xr = p.x + (size_t)m * kHidden;
-            float4_t v[T::FN][4];
+        for (int i = 0; i < T::FN; ++i)
 #pragma unroll
-            for (int i = 0; i < T::FN; ++i)
+            for (int g = 0; g < 4; ++g) {
+                const int n = f.col(i, g);
+                const float4_t b = ld4(p.bias + n), l = ld4(p.ls + n);
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const int n = f.col(i, g);
-                    const float4_t upd = (group4(acc.v[i][j], g) + ld4(p.bias + n)) * ld4(p.ls + n);
-                    const half4_t h = to_half4(widen(*(const half4_t*)(xr + n)) + upd);
-                    *(half4_t*)(xr + n) = h;
-                    v[i][g] = widen(h);
-                }
-            if constexpr (STATS) slot_stats(p.stats, m, f.n_base / 64, v, f.hi);
+                for (int j = 0; j < T::FM; ++j)
+                    *(float4_t*)(st + (j * 32 + f.l32) * SPF + (n - f.n_base)) = (group4(acc.v[i][j], g) + b) * l;
+            }
+        wave_lds_sync();
+        const int lane = threadIdx.x & 63, r0 = lane >> 3, c8 = (lane & 7) * 8;
+#pragma unroll
+        for (int it = 0; it < T::TM / 8; ++it) {
+            const int r = it * 8 + r0, m = f.m_base + r;
+            if (m >= p.rows) continue;  // uniform over the 8 lanes of a row
+            half_t* const xr = p.x + (size_t)m * kHidden + f.n_base + c8;
+            const half8_t old = *(const half8_t*)xr;
+            const float4_t u0 = *(const float4_t*)(st + r * SPF + c8), u1 = *(const float4_t*)(st + r * SPF + c8 + 4);
+            half8_t h;
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                h[e] = (half_t)((float)old[e] + u0[e]);
+                h[e + 4] = (half_t)((float)old[e + 4] + u1[e]);
+            }
+            *(half8_t*)xr = h;
+            if constexpr (STATS) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = (float)h[e];
+                slot_stats(p.stats, m, f.n_base / 64, v, lane & 7);
+            }
         }
     });
 }
 
 // SwiGLU dual GEMM. W rows are packed as blocks of 32 gate rows followed by
 // the 32 matching up rows, so a wave's 64 columns are 32 gate and 32 up
-// columns of the same 32 outputs.
+// columns of the same 32 outputs. The workgroup's BM x BN/2 block of act is
+// staged in LDS and written as whole row pieces of BN bytes.
 template <class T, bool LN>
 __global__ __launch_bounds__(T::THREADS) void swiglu_kernel(SwigluArgs p) {
     static_assert(T::TN == 64, "gate/up pair per wave");
+    constexpr int OW = T::BN / 2;   // act columns per workgroup
+    constexpr int SP = OW + 8;      // staging pitch in halfs
+    constexpr int LPR = OW / 8;     // lanes per row in the copy-out
+    static_assert(T::BM * SP <= T::LDS_HALFS && T::THREADS % LPR == 0, "staging fits the stage buffers");
     __shared__ __attribute__((aligned(16))) half_t lds[T::LDS_HALFS];
     constexpr int NT = 2 * kFF / T::BN;
     ActRows<T> al[2] = {{{}, p.h, kHidden, p.rows, 0}, {{}, p.h, kHidden, p.rows, 0}};
@@ -224,27 +283,42 @@ __global__ __launch_bounds__(T::THREADS) void swiglu_kernel(SwigluArgs p) {
     gemm_tile<T>(al, wl, NT, NT * ((p.rows + T::BM - 1) / T::BM), kHidden / BK, lds,
                        [&](const Acc<T>& acc, int m0, int n0) {
         const Frag<T> f(m0, n0);
-        const int out_base = f.n_base / 2;
+        const int wave = threadIdx.x >> 6;
+        half_t* const st = lds + (wave % T::WGM) * T::TM * SP + (wave / T::WGM) * 32;
+        float4_t bias[2][4], wsum[2][4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int c = g * 8 + f.hi * 4;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                bias[i][g] = ld4(p.bias + f.n_base + 32 * i + c);
+                if constexpr (LN) wsum[i][g] = ld4(p.wsum + f.n_base + 32 * i + c);
+            }
+        }
 #pragma unroll
         for (int j = 0; j < T::FM; ++j) {
-            const int m = f.row(j);
-            if (m >= p.rows) continue;
-            half_t* dst = p.act + (size_t)m * kFF + out_base;
             RowNorm rn{0.f, 1.f};
-            if constexpr (LN) rn = row_norm(p.stats, m);
+            if constexpr (LN) rn = row_norm(p.stats, min(f.row(j), p.rows - 1));
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int c = g * 8 + f.hi * 4;
                 float4_t gate = group4(acc.v[0][j], g), up = group4(acc.v[1][j], g);
                 if constexpr (LN) {
-                    gate = (gate - rn.mean * ld4(p.wsum + f.n_base + c)) * rn.rstd;
-                    up = (up - rn.mean * ld4(p.wsum + f.n_base + 32 + c)) * rn.rstd;
+                    gate = (gate - rn.mean * wsum[0][g]) * rn.rstd;
+                    up = (up - rn.mean * wsum[1][g]) * rn.rstd;
                 }
-                gate += ld4(p.bias + f.n_base + c);
-                up += ld4(p.bias + f.n_base + 32 + c);
+                gate += bias[0][g];
+                up += bias[1][g];
                 const float4_t y = float4_t{silu(gate[0]), silu(gate[1]), silu(gate[2]), silu(gate[3])} * up;
-                *(half4_t*)(dst + c) = to_half4(y);
+                *(half4_t*)(st + (j * 32 + f.l32) * SP + c) = to_half4(y);
             }
+        }
+        lds_barrier();
+        const int r0 = threadIdx.x / LPR, c8 = (threadIdx.x % LPR) * 8;
+#pragma unroll
+        for (int it = 0; it < T::BM * LPR / T::THREADS; ++it) {
+            const int r = it * (T::THREADS / LPR) + r0, m = m0 + r;
+            if (m < p.rows) *(half8_t*)(p.act + (size_t)m * kFF + n0 / 2 + c8) = *(const half8_t*)(lds + r * SP + c8);
         }
     });
 }

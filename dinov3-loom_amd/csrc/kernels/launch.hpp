@@ -45,8 +45,10 @@ constexpr int kStatSlots = kHidden / 64;
 constexpr int kStatFloats = 2 * kStatSlots;
 
 // h [rows][384] f16 . Wqkv[1152][384]^T + b, 2D RoPE on q and k of patch
-// tokens, written head-major: q, k [images][6][tpad][64]; v transposed as
-// vt [images][6][64][tpad].
+// tokens, written head-major: q, k, v [images][6][tpad][64] (rows past the
+// image's tokens are never written). cos / sin are [patches][64] with columns
+// 32..63 repeating 0..31 (the rotation of channels c and c+32 uses angle c);
+// only columns 0..31 are read.
 // With stats == nullptr: h = LN1(x) is given and out = h.W^T + bias. With
 // stats: h is the raw residual x, w holds W' = gamma (.) W (per input
 // channel), wsum[n] = sum_k W'[n][k] and bias holds t = b + beta.W^T, so
@@ -59,7 +61,7 @@ struct QkvArgs {
     const float* sin;
     half_t* q;
     half_t* k;
-    half_t* vt;
+    half_t* v;
     int images;
     int grid;
     int tpad;
@@ -67,12 +69,14 @@ struct QkvArgs {
     const float* wsum = nullptr;
 };
 
-// softmax(q k^T / 8) v per (image, head) over that image's T tokens;
+// softmax(q k^T / 8) v per (image, head) over that image's T tokens, with
+// q, k, v as written by the QKV kernel; rows T .. tpad-1 of v must be finite
+// (the engine zeroes buffers at allocation and nothing writes those rows).
 // out [images*T][384] f16 (head h in columns 64h .. 64h+63).
 struct AttentionArgs {
     const half_t* q;
     const half_t* k;
-    const half_t* vt;
+    const half_t* v;
     half_t* out;
     int images;
     int tokens;

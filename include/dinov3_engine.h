@@ -37,8 +37,8 @@ typedef struct dhx_region {
  *   DHX_K_LAYERNORM     s = {rows}                   b = {x f16, gamma f32, beta f32, out f16}
  *   DHX_K_LAYERNORM_F32 s = {rows}                   b = {x f16, gamma f32, beta f32, out f32}
  *   DHX_K_QKV_ROPE      s = {images, grid, tpad}     b = {h f16, qkv_w f16 [1152][384], qkv_b f32,
- *                                                          rope_cos f32 [P][64], rope_sin f32, q, k, vt}
- *   DHX_K_ATTENTION     s = {images, grid, tpad}     b = {q, k, vt, out f16 [rows][384]}
+ *                                                          rope_cos f32 [P][64], rope_sin f32, q, k, v}
+ *   DHX_K_ATTENTION     s = {images, grid, tpad}     b = {q, k, v, out f16 [rows][384]}
  *   DHX_K_RESID         s = {rows, k}                b = {a f16 [rows][k], w f16 [384][k], b f32, ls f32, x f16}
  *   DHX_K_SWIGLU        s = {rows}                   b = {h f16, gateup_w f16 [3072][384], gateup_b f32, act f16}
  *   DHX_K_SPLITK        s = {rows, k, splits}        b = {a f16, w f16 [384][k], partials f32 [splits][rows][384]}
@@ -46,7 +46,7 @@ typedef struct dhx_region {
  *   DHX_K_PATCH_EMBED_STATS   s = {images, grid}   b = {pixels, patch_w, patch_b, prefix, prefix_stats f32 [5][12],
  *                                                        x f16, stats f32 [rows][12]}
  *   DHX_K_QKV_ROPE_LN         s = {images, grid, tpad}  b = {x f16, stats, qkv_wln f16 [1152][384], qkv_wsum f32,
- *                                                        qkv_t f32, rope_cos, rope_sin, q, k, vt}
+ *                                                        qkv_t f32, rope_cos, rope_sin, q, k, v}
  *   DHX_K_RESID_STATS         s = {rows, k}        b = {a, w, b, ls, x, stats}
  *   DHX_K_SWIGLU_LN           s = {rows}           b = {x f16, stats, gateup_wln f16 [3072][384], gateup_wsum f32,
  *                                                        gateup_t f32, act}
@@ -57,8 +57,11 @@ typedef struct dhx_region {
  * input algebraically from those statistics: with W' = gamma (.) W (f16),
  * wsum[n] = sum_k W'[n][k] and t = b + beta . W^T, out = rstd * (x . W'^T -
  * mean * wsum) + t equals LN(x) . W^T + b.
- * q and k are [images][6][tpad][64] f16, vt is [images][6][64][tpad] f16,
- * tpad a multiple of 128 >= T = grid*grid + 5; k (and k / splits) a multiple
+ * q, k and v are [images][6][tpad][64] f16 (rows T .. tpad-1 are never
+ * written and must hold finite values for attention: regions from
+ * dhx_allocate start zeroed), tpad a multiple of 128 >= T = grid*grid + 5;
+ * the RoPE tables hold one row of 64 angles per patch whose columns 32..63
+ * repeat 0..31 (as DINOv3's do); the kernels read columns 0..31; k (and k / splits) a multiple
  * of 128 (the GEMM K loop runs stages of 64 in pairs). Every binding's size is
  * checked against these shapes before anything is launched or recorded. */
 enum {

@@ -65,6 +65,17 @@ def check(gpu, ref, atol, rel=2.0**-10, cos_min=0.99999, what=""):
     return err.max()
 
 
+def test_allocation_fill_is_ordered_before_upload(eng):
+    # dhx_allocate zeroes a new region; the fill must complete before an
+    # upload queued right after it (on the engine's own stream), or the
+    # zeros could land on top of the uploaded bytes.
+    rng = np.random.default_rng(3)
+    for _ in range(6):
+        a = rng.integers(1, 255, size=48 << 20, dtype=np.uint8)
+        r = up(eng, a)
+        assert np.array_equal(eng.read(r, np.uint8, a.shape), a)
+
+
 @pytest.mark.parametrize("rows", [1, 1001, 12864])
 @pytest.mark.parametrize("f32_out", [False, True])
 def test_layernorm(eng, rows, f32_out):
@@ -132,12 +143,18 @@ def test_qkv_rope(eng, images, grid):
     w = f16(rng.normal(size=(1152, 384)) * 0.05)
     b = (rng.normal(size=1152) * 0.1).astype(np.float32)
     cos, sin = oracle.rope_tables(grid)
+    # The kernel reads angle columns 0..31 only (DINOv3's tables repeat them
+    # in 32..63): poisoned upper halves must not reach the output.
+    assert np.array_equal(cos[:, :32], cos[:, 32:]) and np.array_equal(sin[:, :32], sin[:, 32:])
+    cos, sin = cos.copy(), sin.copy()
+    cos[:, 32:] = np.nan
+    sin[:, 32:] = np.nan
     nb = images * 6 * tpad * 64 * 2
-    q, k, vt = eng.allocate(nb), eng.allocate(nb), eng.allocate(nb)
-    run(eng, K_QKV, [images, grid, tpad], [up(eng, h), up(eng, w), up(eng, b), up(eng, cos), up(eng, sin), q, k, vt])
+    q, k, v = eng.allocate(nb), eng.allocate(nb), eng.allocate(nb)
+    run(eng, K_QKV, [images, grid, tpad], [up(eng, h), up(eng, w), up(eng, b), up(eng, cos), up(eng, sin), q, k, v])
     gq = eng.read(q, np.float16, (images, 6, tpad, 64))
     gk = eng.read(k, np.float16, (images, 6, tpad, 64))
-    gv = eng.read(vt, np.float16, (images, 6, 64, tpad))
+    gv = eng.read(v, np.float16, (images, 6, tpad, 64))
     hd = h.astype(np.float64)
     for i in range(images):
         rows = hd[i * T:(i + 1) * T]
@@ -147,9 +164,9 @@ def test_qkv_rope(eng, images, grid):
         to_tok = lambda a: a.transpose(1, 0, 2).reshape(T, 384)
         check(to_tok(gq[i, :, :T]), rq, atol=1e-3, what=f"q img {i}")
         check(to_tok(gk[i, :, :T]), rk, atol=1e-3, what=f"k img {i}")
-        check(gv[i, :, :, :T].transpose(2, 0, 1).reshape(T, 384), rv, atol=1e-3, what=f"v img {i}")
-    # padded rows / columns are never written
-    assert not gq[:, :, T:].any() and not gk[:, :, T:].any() and not gv[:, :, :, T:].any()
+        check(to_tok(gv[i, :, :T]), rv, atol=1e-3, what=f"v img {i}")
+    # padded rows are never written
+    assert not gq[:, :, T:].any() and not gk[:, :, T:].any() and not gv[:, :, T:].any()
 
 
 @pytest.mark.parametrize("images,grid,qscale", [(2, 14, 2.0), (1, 32, 2.0), (3, 4, 4.0), (1, 14, 0.0)])
@@ -160,10 +177,10 @@ def test_attention(eng, images, grid, qscale):
     q = f16(rng.normal(size=(images * T, 384)) * qscale)
     k = f16(rng.normal(size=(images * T, 384)))
     v = f16(rng.normal(size=(images * T, 384)))
-    vt = head_major(v, images, T, tpad).transpose(0, 1, 3, 2).copy()
     out = eng.allocate(images * T * 384 * 2)
     run(eng, K_ATTN, [images, grid, tpad],
-        [up(eng, head_major(q, images, T, tpad)), up(eng, head_major(k, images, T, tpad)), up(eng, vt), out])
+        [up(eng, head_major(q, images, T, tpad)), up(eng, head_major(k, images, T, tpad)),
+         up(eng, head_major(v, images, T, tpad)), out])
     y = eng.read(out, np.float16, (images * T, 384))
     for i in range(images):
         sl = slice(i * T, (i + 1) * T)
@@ -345,19 +362,19 @@ def test_qkv_rope_layernorm_fused(eng, images, grid, offset):
     wl, wsum, t = fold(w, b, gamma, beta)
     cos, sin = oracle.rope_tables(grid)
     nb = images * 6 * tpad * 64 * 2
-    q, k, vt = eng.allocate(nb), eng.allocate(nb), eng.allocate(nb)
+    q, k, v = eng.allocate(nb), eng.allocate(nb), eng.allocate(nb)
     run(eng, K_QKV_LN, [images, grid, tpad],
         [up(eng, x), up(eng, slot_stats(x)), up(eng, wl), up(eng, wsum), up(eng, t), up(eng, cos), up(eng, sin),
-         q, k, vt])
+         q, k, v])
     gq = eng.read(q, np.float16, (images, 6, tpad, 64))
-    gv = eng.read(vt, np.float16, (images, 6, 64, tpad))
+    gv = eng.read(v, np.float16, (images, 6, tpad, 64))
     h = oracle.layernorm(x.astype(np.float64), gamma, beta)  # LN(x), unrounded
     for i in range(images):
         rows = h[i * T:(i + 1) * T]
         rq = oracle.rope(oracle.linear(rows, w[:384].astype(np.float64), b[:384]), grid)
         rv = oracle.linear(rows, w[768:].astype(np.float64), b[768:])
         check(gq[i, :, :T].transpose(1, 0, 2).reshape(T, 384), rq, atol=3e-3, what=f"fused-LN q img {i}")
-        check(gv[i, :, :, :T].transpose(2, 0, 1).reshape(T, 384), rv, atol=3e-3, what=f"fused-LN v img {i}")
+        check(gv[i, :, :T].transpose(1, 0, 2).reshape(T, 384), rv, atol=3e-3, what=f"fused-LN v img {i}")
 
 
 @pytest.mark.parametrize("rows,offset", [(1001, 0.0), (12864, 2.0)])
