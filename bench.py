@@ -107,6 +107,8 @@ def main():
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--branches", type=int, default=0,
+                    help="image groups run as concurrent graph branches (0: pick 1-4 by a short trial)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (images shard across GPUs with no "
@@ -122,15 +124,21 @@ def main():
         model = d.DINOv3.load(path, d.Options(device=0, max_batch=max(b, 32)))
         px = d.random_pixels(1, b)
 
-        # Pick the down-projection variant for this batch by a short trial
-        # (the reference uses the residual GEMM for b > 1, split-K at b = 1).
+        # Pick the down-projection variant (the reference uses the residual
+        # GEMM for b > 1, split-K at b = 1) and the number of image groups run
+        # side by side by a short trial; every choice gives the same bits.
         trial = {}
         for mode in (0, 1):
-            model.set_splitk(mode)
-            model.stage(px)
-            trial[mode] = timed_replays(model, b, 10)
-        mode = min(trial, key=trial.get)
+            for nb in ([args.branches] if args.branches else [1, 2, 3, 4]):
+                model.set_splitk(mode)
+                model.set_branches(nb)
+                model.stage(px)
+                trial[(mode, nb)] = timed_replays(model, b, 10)
+        mode, branches = min(trial, key=trial.get)
+        print(json.dumps({"trial_images_per_s": {f"{'splitk' if k[0] else 'resid'}/{k[1]}": round(b / v, 1)
+                                                 for k, v in trial.items()}}), file=sys.stderr)
         model.set_splitk(mode)
+        model.set_branches(branches)
         model.stage(px)
         for _ in range(args.warmup):
             model.replay(b)
@@ -143,7 +151,10 @@ def main():
             model.replay(32)
         sec32 = timed_replays(model, 32, args.steps)
 
-        # Per-launch device time (HIP events on the model's stream).
+        # Per-launch device time (HIP events on the model's stream), each
+        # kernel alone over the whole batch: the single-group plan.
+        model.set_branches(1)
+        model.stage(px)
         launches = model.launch_timings(b, iters=20)
         kernels = {}
         for i, (name, ms) in enumerate(launches):
@@ -190,7 +201,8 @@ def main():
         "vs_baseline": None, "dtype": "f16", "data": "synthetic",
         "config": {"workload": f"DINOv3 ViT-S+/16 forward, 224x224, batch {b}, resident hipGraph replay "
                                "(BASELINE.json config 3)", "batch": b, "image_size": 224, "tokens": T,
-                   "down_proj": "splitk" if mode == 1 else "resid", "weights": "seeded random init (BASELINE)"},
+                   "down_proj": "splitk" if mode == 1 else "resid", "branches": branches,
+                   "weights": "seeded random init (BASELINE)"},
         "mfma_frac_forward": round(value * GFLOP_PER_IMAGE / 1e3 / PEAK_TFLOPS, 4),
         "batch32": {"value": round(32 / sec32, 1), "ms_per_step": round(sec32 * 1e3, 4)},
         "roofline": roof,

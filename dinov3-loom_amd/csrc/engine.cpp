@@ -23,7 +23,8 @@ constexpr char kPoisoned[] = "session is unusable after a GPU failure";
 
 struct Recorded {
     hipGraphExec_t exec = nullptr;
-    std::vector<dhx_launch> launches;
+    std::vector<dhx_launch> launches;  // the branches' lists back to back
+    std::vector<uint64_t> counts;      // launches per branch
 };
 
 }  // namespace
@@ -31,6 +32,12 @@ struct Recorded {
 struct dhx_engine {
     int device = 0;
     hipStream_t stream = nullptr;
+    // Extra streams and events for plans with several branches: branch 0
+    // runs on `stream`, branch i on aux[i-1], forked from and joined back
+    // into `stream` with events (created on first use; default priority).
+    std::vector<hipStream_t> aux;
+    hipEvent_t fork = nullptr;
+    std::vector<hipEvent_t> join;
     std::vector<void*> buffers;
     std::vector<uint64_t> sizes;
     std::map<uint64_t, Recorded> graphs;
@@ -168,7 +175,7 @@ void validate(const dhx_engine* e, const dhx_launch& l) {
     }
 }
 
-hipError_t launch_one(dhx_engine* e, const dhx_launch& l) {
+hipError_t launch_one(dhx_engine* e, const dhx_launch& l, hipStream_t stream) {
     using namespace dhx;
     auto P = [&](int i) { return region_ptr(e, l.bindings[i]); };
     auto F = [&](int i) { return static_cast<const float*>(P(i)); };
@@ -177,42 +184,80 @@ hipError_t launch_one(dhx_engine* e, const dhx_launch& l) {
     auto Fm = [&](int i) { return static_cast<float*>(P(i)); };
     switch (l.kernel) {
         case DHX_K_PATCH_EMBED:
-            return launch_patch_embed({F(0), Hf(1), F(2), F(3), Hf(4), (int)s[0], (int)s[1]}, e->stream);
+            return launch_patch_embed({F(0), Hf(1), F(2), F(3), Hf(4), (int)s[0], (int)s[1]}, stream);
         case DHX_K_PATCH_EMBED_STATS:
-            return launch_patch_embed({F(0), Hf(1), F(2), F(3), Hf(5), (int)s[0], (int)s[1], F(4), Fm(6)}, e->stream);
+            return launch_patch_embed({F(0), Hf(1), F(2), F(3), Hf(5), (int)s[0], (int)s[1], F(4), Fm(6)}, stream);
         case DHX_K_LAYERNORM:
         case DHX_K_LAYERNORM_F32:
-            return launch_layernorm({Hf(0), F(1), F(2), P(3), (int)s[0], l.kernel == DHX_K_LAYERNORM_F32}, e->stream);
+            return launch_layernorm({Hf(0), F(1), F(2), P(3), (int)s[0], l.kernel == DHX_K_LAYERNORM_F32}, stream);
         case DHX_K_QKV_ROPE:
             return launch_qkv_rope({Hf(0), Hf(1), F(2), F(3), F(4), Hf(5), Hf(6), Hf(7), (int)s[0], (int)s[1], (int)s[2]},
-                                   e->stream);
+                                   stream);
         case DHX_K_QKV_ROPE_LN:
             return launch_qkv_rope({Hf(0), Hf(2), F(4), F(5), F(6), Hf(7), Hf(8), Hf(9), (int)s[0], (int)s[1], (int)s[2],
                                     F(1), F(3)},
-                                   e->stream);
+                                   stream);
         case DHX_K_ATTENTION:
-            return launch_attention({Hf(0), Hf(1), Hf(2), Hf(3), (int)s[0], (int)tokens_for(s[1]), (int)s[2]}, e->stream);
+            return launch_attention({Hf(0), Hf(1), Hf(2), Hf(3), (int)s[0], (int)tokens_for(s[1]), (int)s[2]}, stream);
         case DHX_K_RESID:
-            return launch_resid({Hf(0), Hf(1), F(2), F(3), Hf(4), (int)s[0], (int)s[1]}, e->stream);
+            return launch_resid({Hf(0), Hf(1), F(2), F(3), Hf(4), (int)s[0], (int)s[1]}, stream);
         case DHX_K_RESID_STATS:
-            return launch_resid({Hf(0), Hf(1), F(2), F(3), Hf(4), (int)s[0], (int)s[1], Fm(5)}, e->stream);
+            return launch_resid({Hf(0), Hf(1), F(2), F(3), Hf(4), (int)s[0], (int)s[1], Fm(5)}, stream);
         case DHX_K_SWIGLU:
-            return launch_swiglu({Hf(0), Hf(1), F(2), Hf(3), (int)s[0]}, e->stream);
+            return launch_swiglu({Hf(0), Hf(1), F(2), Hf(3), (int)s[0]}, stream);
         case DHX_K_SWIGLU_LN:
-            return launch_swiglu({Hf(0), Hf(2), F(4), Hf(5), (int)s[0], F(1), F(3)}, e->stream);
+            return launch_swiglu({Hf(0), Hf(2), F(4), Hf(5), (int)s[0], F(1), F(3)}, stream);
         case DHX_K_SPLITK:
-            return launch_splitk({Hf(0), Hf(1), (float*)P(2), (int)s[0], (int)s[1], (int)s[2]}, e->stream);
+            return launch_splitk({Hf(0), Hf(1), (float*)P(2), (int)s[0], (int)s[1], (int)s[2]}, stream);
         case DHX_K_SPLITK_REDUCE:
-            return launch_splitk_reduce({F(0), F(1), F(2), Hf(3), (int)s[0], (int)s[1]}, e->stream);
+            return launch_splitk_reduce({F(0), F(1), F(2), Hf(3), (int)s[0], (int)s[1]}, stream);
         case DHX_K_SPLITK_REDUCE_STATS:
-            return launch_splitk_reduce({F(0), F(1), F(2), Hf(3), (int)s[0], (int)s[1], Fm(4)}, e->stream);
+            return launch_splitk_reduce({F(0), F(1), F(2), Hf(3), (int)s[0], (int)s[1], Fm(4)}, stream);
         default:
             return hipErrorInvalidValue;
     }
 }
 
-void run_list(dhx_engine* e, const std::vector<dhx_launch>& launches) {
-    for (const dhx_launch& l : launches) hip_check(e, launch_one(e, l), "kernel launch");
+// Streams and events for `branches` concurrent lists.
+void ensure_branch_streams(dhx_engine* e, uint32_t branches) {
+    if (!e->fork) hip_check(e, hipEventCreateWithFlags(&e->fork, hipEventDisableTiming), "hipEventCreate");
+    while (e->aux.size() + 1 < branches) {
+        hipStream_t s = nullptr;
+        hip_check(e, hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate");
+        e->aux.push_back(s);
+        hipEvent_t ev = nullptr;
+        hip_check(e, hipEventCreateWithFlags(&ev, hipEventDisableTiming), "hipEventCreate");
+        e->join.push_back(ev);
+    }
+}
+
+// Queues the branches of a plan: branch 0 on the engine stream, the others
+// forked from it onto the auxiliary streams and joined back, so work queued
+// on the engine stream afterwards waits for every branch. Used both under
+// stream capture (the fork/join become graph edges) and for direct dispatch.
+// Returns the first launch error; the fork/join structure is completed even
+// then so that a capture can still be ended.
+hipError_t queue_branches(dhx_engine* e, const Recorded& r) {
+    const size_t n = r.counts.size();
+    hipError_t err = hipSuccess;
+    auto keep = [&](hipError_t x) {
+        if (err == hipSuccess) err = x;
+    };
+    if (n > 1) {
+        keep(hipEventRecord(e->fork, e->stream));
+        for (size_t i = 1; i < n; ++i) keep(hipStreamWaitEvent(e->aux[i - 1], e->fork, 0));
+    }
+    size_t first = 0;
+    for (size_t i = 0; i < n; ++i) {
+        hipStream_t s = i == 0 ? e->stream : e->aux[i - 1];
+        for (size_t j = first; j < first + r.counts[i] && err == hipSuccess; ++j) keep(launch_one(e, r.launches[j], s));
+        first += r.counts[i];
+    }
+    for (size_t i = 1; i < n; ++i) {
+        keep(hipEventRecord(e->join[i - 1], e->aux[i - 1]));
+        keep(hipStreamWaitEvent(e->stream, e->join[i - 1], 0));
+    }
+    return err;
 }
 
 void set_device(dhx_engine* e) { hip_check(e, hipSetDevice(e->device), "hipSetDevice"); }
@@ -277,6 +322,12 @@ void dhx_engine_free(dhx_engine* e) {
         if (kv.second.exec) (void)hipGraphExecDestroy(kv.second.exec);
     for (void* b : e->buffers) (void)hipFree(b);
     if (e->readback) (void)hipHostFree(e->readback);
+    for (hipStream_t s : e->aux) {
+        (void)hipStreamSynchronize(s);
+        (void)hipStreamDestroy(s);
+    }
+    for (hipEvent_t ev : e->join) (void)hipEventDestroy(ev);
+    if (e->fork) (void)hipEventDestroy(e->fork);
     if (e->stream) (void)hipStreamDestroy(e->stream);
     delete e;
 }
@@ -321,21 +372,28 @@ int dhx_upload(dhx_engine* e, dhx_region r, const void* bytes, uint64_t n) {
     });
 }
 
-int dhx_record(dhx_engine* e, uint64_t batch, const dhx_launch* launches, uint64_t n) {
+int dhx_record_branches(dhx_engine* e, uint64_t batch, const dhx_launch* launches, const uint64_t* counts,
+                        uint32_t branches) {
     return guarded(e, [&] {
         ensure_usable(e);
         if (e->graphs.count(batch)) return;
-        std::vector<dhx_launch> list(launches, launches + n);
-        for (const dhx_launch& l : list) validate(e, l);  // before any GPU work
+        if (branches < 1 || branches > DHX_MAX_BRANCHES)
+            throw dhx::Error("branches must be 1.." + std::to_string(DHX_MAX_BRANCHES));
+        if (!counts) throw dhx::Error("null branch counts");
+        Recorded rec;
+        rec.counts.assign(counts, counts + branches);
+        uint64_t n = 0;
+        for (uint64_t c : rec.counts) n += c;
+        if (n && !launches) throw dhx::Error("null launch list");
+        rec.launches.assign(launches, launches + n);
+        for (const dhx_launch& l : rec.launches) validate(e, l);  // before any GPU work
         set_device(e);
-        // One linear chain on one stream: each node follows its predecessor,
-        // covering every read-before-write on reused buffers (engine.rs:110-111).
+        ensure_branch_streams(e, branches);
+        // Within a branch each node follows its predecessor, covering every
+        // read-before-write on reused buffers (engine.rs:110-111); branches
+        // are forked from and joined back into the capturing stream.
         hip_check(e, hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal), "begin capture");
-        hipError_t launch_err = hipSuccess;
-        for (const dhx_launch& l : list) {
-            launch_err = launch_one(e, l);
-            if (launch_err != hipSuccess) break;
-        }
+        const hipError_t launch_err = queue_branches(e, rec);
         hipGraph_t graph = nullptr;
         const hipError_t end_err = hipStreamEndCapture(e->stream, &graph);
         if (launch_err != hipSuccess || end_err != hipSuccess) {
@@ -346,8 +404,13 @@ int dhx_record(dhx_engine* e, uint64_t batch, const dhx_launch* launches, uint64
         const hipError_t inst = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
         (void)hipGraphDestroy(graph);
         hip_check(e, inst, "graph instantiate");
-        e->graphs[batch] = Recorded{exec, std::move(list)};
+        rec.exec = exec;
+        e->graphs[batch] = std::move(rec);
     });
+}
+
+int dhx_record(dhx_engine* e, uint64_t batch, const dhx_launch* launches, uint64_t n) {
+    return dhx_record_branches(e, batch, launches, &n, 1);
 }
 
 int dhx_has_graph(const dhx_engine* e, uint64_t batch) { return e && e->graphs.count(batch) ? 1 : 0; }
@@ -368,7 +431,7 @@ int dhx_dispatch(dhx_engine* e, uint64_t batch) {
         auto it = e->graphs.find(batch);
         if (it == e->graphs.end()) throw dhx::Error("batch has not been prepared");
         set_device(e);
-        run_list(e, it->second.launches);
+        hip_check(e, queue_branches(e, it->second), "kernel launch");
     });
 }
 
@@ -421,7 +484,7 @@ int dhx_benchmark(dhx_engine* e, uint64_t batch, uint64_t samples, dhx_timings* 
             for (int mode : order) {
                 const auto start = std::chrono::steady_clock::now();
                 if (mode == 0) hip_check(e, hipGraphLaunch(it->second.exec, e->stream), "graph launch");
-                else run_list(e, it->second.launches);
+                else hip_check(e, queue_branches(e, it->second), "kernel launch");
                 hip_check(e, hipStreamSynchronize(e->stream), "synchronize");
                 const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - start).count();
                 if (i >= 10) times[mode].push_back(ms);
@@ -449,9 +512,9 @@ int dhx_launch_timings(dhx_engine* e, uint64_t batch, uint32_t iters, double* ms
         hip_check(e, hipEventCreate(&a), "hipEventCreate");
         hip_check(e, hipEventCreate(&b), "hipEventCreate");
         for (size_t i = 0; i < list.size(); ++i) {
-            hip_check(e, launch_one(e, list[i]), "kernel launch");  // warm
+            hip_check(e, launch_one(e, list[i], e->stream), "kernel launch");  // warm
             hip_check(e, hipEventRecord(a, e->stream), "hipEventRecord");
-            for (uint32_t k = 0; k < iters; ++k) hip_check(e, launch_one(e, list[i]), "kernel launch");
+            for (uint32_t k = 0; k < iters; ++k) hip_check(e, launch_one(e, list[i], e->stream), "kernel launch");
             hip_check(e, hipEventRecord(b, e->stream), "hipEventRecord");
             hip_check(e, hipEventSynchronize(b), "hipEventSynchronize");
             float ms = 0.f;

@@ -27,6 +27,8 @@ namespace {
 
 constexpr uint64_t kHiddenU = 384;
 constexpr uint32_t kSplits = 4;
+// Smallest image group worth its own branch of the plan.
+constexpr uint64_t kMinBranchImages = 4;
 
 // hub.rs:7-11
 constexpr char kRepoOwner[] = "facebook";
@@ -93,7 +95,7 @@ public:
         }
         const uint64_t B = opts.max_batch, r = B * tokens_;
         const uint64_t heads = B * 6 * tpad_ * 64 * 2;
-        // x, h, attn and act are f16; q/k/v^T are f16 head-major (padded rows
+        // x, h, attn and act are f16; q/k/v are f16 head-major (padded rows
         // stay zero); out, the NCHW images, the split-K slabs and the
         // LayerNorm row statistics of x are f32.
         const uint64_t sizes[kBuffers] = {r * kHiddenU * 2, r * kHiddenU * 2, heads, heads, heads, r * kHiddenU * 2,
@@ -115,6 +117,11 @@ public:
     void set_layernorm_fusion(int on) {
         if (on != 0 && on != 1) throw Error("layernorm fusion must be 0 or 1");
         fused_ln_ = on;
+    }
+
+    void set_branches(uint32_t n) {
+        if (n < 1 || n > DHX_MAX_BRANCHES) throw Error("branches must be 1.." + std::to_string(DHX_MAX_BRANCHES));
+        branches_ = n;
     }
 
     // lib.rs:90-114
@@ -155,17 +162,35 @@ public:
         check(dhx_benchmark(engine_.get(), key(n / image_elems_), samples, out), engine_.get());
     }
 
-    // lib.rs:149-263 (prepare): one launch list per batch size, recorded as
-    // one graph. The down projection uses split-K slabs + reduce at batch 1
-    // (as the reference) or when selected, else the residual GEMM. By
-    // default LayerNorm is folded into the QKV and gate/up GEMMs, fed by row
-    // statistics that the producers of x write (62 launches at b > 1); the
-    // unfused plan runs LayerNorm kernels as the reference does (86).
+    // lib.rs:149-263 (prepare): one launch plan per batch size, recorded as
+    // one graph. The batch is cut into `branches_` groups of images (for
+    // b >= 2 * kMinBranchImages) that run as independent chains, each over
+    // its own slice of every buffer: the kernels of one group fill the last,
+    // partial wave of workgroups of the other's. A row's arithmetic does not
+    // depend on the group it is in, so results are bitwise the same. The down
+    // projection uses split-K slabs + reduce at batch 1 (as the reference) or
+    // when selected, else the residual GEMM. By default LayerNorm is folded
+    // into the QKV and gate/up GEMMs, fed by row statistics that the
+    // producers of x write (62 launches per group at b > 1); the unfused plan
+    // runs LayerNorm kernels as the reference does (86).
     void prepare(uint64_t b) {
         if (dhx_has_graph(engine_.get(), key(b))) return;
-        const uint32_t r = (uint32_t)(b * tokens_);
-        const uint32_t B = (uint32_t)b, G = grid_, TP = (uint32_t)tpad_;
+        const uint32_t nb = groups(b);
         std::vector<dhx_launch> l;
+        std::vector<uint64_t> counts;
+        for (uint32_t g = 0; g < nb; ++g) {
+            const uint64_t first = b * g / nb, end = b * (g + 1) / nb;
+            const size_t before = l.size();
+            plan(first, end - first, b, l);
+            counts.push_back(l.size() - before);
+        }
+        check(dhx_record_branches(engine_.get(), key(b), l.data(), counts.data(), nb), engine_.get());
+    }
+
+    // The launches for images [first, first + n) of a batch of b.
+    void plan(uint64_t first, uint64_t n, uint64_t b, std::vector<dhx_launch>& l) const {
+        const uint32_t r = (uint32_t)(n * tokens_);
+        const uint32_t B = (uint32_t)n, G = grid_, TP = (uint32_t)tpad_;
         auto add = [&](uint32_t kernel, std::initializer_list<uint32_t> s, std::initializer_list<dhx_region> bind) {
             dhx_launch x{};
             x.kernel = kernel;
@@ -176,13 +201,25 @@ public:
             l.push_back(x);
         };
         auto w = [&](const std::string& name) { return weights_.at(name); };
+        // This group's slice of a buffer holding `per_image` bytes per image.
+        auto part = [&](int buf, uint64_t per_image) {
+            dhx_region g = a_[buf];
+            g.offset += first * per_image;
+            g.bytes = n * per_image;
+            return g;
+        };
+        const uint64_t row = tokens_ * kHiddenU;
+        const uint64_t heads = 6 * tpad_ * 64 * 2;
+        const dhx_region X = part(kX, row * 2), H = part(kH, row * 2), S = part(kStats, tokens_ * 12 * 4);
+        const dhx_region Q = part(kQ, heads), K = part(kK, heads), V = part(kV, heads);
+        const dhx_region A = part(kAttn, row * 2), F = part(kAct, tokens_ * 1536 * 2);
+        const dhx_region O = part(kOut, row * 4), I = part(kImage, image_elems_ * 4);
+        const dhx_region SL = part(kPartials, (uint64_t)kSplits * row * 4);  // [splits][rows][384] per group
         const bool split = b == 1 || splitk_ == 1;
-        const dhx_region X = region(kX), H = region(kH), S = region(kStats);
         if (fused_ln_) {
-            add(DHX_K_PATCH_EMBED_STATS, {B, G},
-                {region(kImage), w("patch_w"), w("patch_b"), w("prefix"), w("prefix_stats"), X, S});
+            add(DHX_K_PATCH_EMBED_STATS, {B, G}, {I, w("patch_w"), w("patch_b"), w("prefix"), w("prefix_stats"), X, S});
         } else {
-            add(DHX_K_PATCH_EMBED, {B, G}, {region(kImage), w("patch_w"), w("patch_b"), w("prefix"), X});
+            add(DHX_K_PATCH_EMBED, {B, G}, {I, w("patch_w"), w("patch_b"), w("prefix"), X});
             add(DHX_K_LAYERNORM, {r}, {X, w("l0_norm1_w"), w("l0_norm1_b"), H});
         }
         for (int i = 0; i < 12; ++i) {
@@ -190,53 +227,54 @@ public:
             const bool last = i == 11;
             if (fused_ln_)
                 add(DHX_K_QKV_ROPE_LN, {B, G, TP},
-                    {X, S, w(p + "qkv_wln"), w(p + "qkv_wsum"), w(p + "qkv_t"), w("rope_cos"), w("rope_sin"),
-                     region(kQ), region(kK), region(kVt)});
+                    {X, S, w(p + "qkv_wln"), w(p + "qkv_wsum"), w(p + "qkv_t"), w("rope_cos"), w("rope_sin"), Q, K, V});
             else
                 add(DHX_K_QKV_ROPE, {B, G, TP},
-                    {H, w(p + "qkv_w"), w(p + "qkv_b"), w("rope_cos"), w("rope_sin"), region(kQ), region(kK),
-                     region(kVt)});
-            add(DHX_K_ATTENTION, {B, G, TP}, {region(kQ), region(kK), region(kVt), region(kAttn)});
+                    {H, w(p + "qkv_w"), w(p + "qkv_b"), w("rope_cos"), w("rope_sin"), Q, K, V});
+            add(DHX_K_ATTENTION, {B, G, TP}, {Q, K, V, A});
             if (fused_ln_) {
-                add(DHX_K_RESID_STATS, {r, 384}, {region(kAttn), w(p + "o_w"), w(p + "o_b"), w(p + "ls1"), X, S});
-                add(DHX_K_SWIGLU_LN, {r},
-                    {X, S, w(p + "gateup_wln"), w(p + "gateup_wsum"), w(p + "gateup_t"), region(kAct)});
+                add(DHX_K_RESID_STATS, {r, 384}, {A, w(p + "o_w"), w(p + "o_b"), w(p + "ls1"), X, S});
+                add(DHX_K_SWIGLU_LN, {r}, {X, S, w(p + "gateup_wln"), w(p + "gateup_wsum"), w(p + "gateup_t"), F});
             } else {
-                add(DHX_K_RESID, {r, 384}, {region(kAttn), w(p + "o_w"), w(p + "o_b"), w(p + "ls1"), X});
+                add(DHX_K_RESID, {r, 384}, {A, w(p + "o_w"), w(p + "o_b"), w(p + "ls1"), X});
                 add(DHX_K_LAYERNORM, {r}, {X, w(p + "norm2_w"), w(p + "norm2_b"), H});
-                add(DHX_K_SWIGLU, {r}, {H, w(p + "gateup_w"), w(p + "gateup_b"), region(kAct)});
+                add(DHX_K_SWIGLU, {r}, {H, w(p + "gateup_w"), w(p + "gateup_b"), F});
             }
             // The last block's statistics would have no reader (the final
             // LayerNorm computes its own).
             const bool stats = fused_ln_ && !last;
             if (split) {
-                add(DHX_K_SPLITK, {r, 1536, kSplits}, {region(kAct), w(p + "down_w"), region(kPartials)});
+                add(DHX_K_SPLITK, {r, 1536, kSplits}, {F, w(p + "down_w"), SL});
                 if (stats)
-                    add(DHX_K_SPLITK_REDUCE_STATS, {r, kSplits},
-                        {region(kPartials), w(p + "down_b"), w(p + "ls2"), X, S});
+                    add(DHX_K_SPLITK_REDUCE_STATS, {r, kSplits}, {SL, w(p + "down_b"), w(p + "ls2"), X, S});
                 else
-                    add(DHX_K_SPLITK_REDUCE, {r, kSplits}, {region(kPartials), w(p + "down_b"), w(p + "ls2"), X});
+                    add(DHX_K_SPLITK_REDUCE, {r, kSplits}, {SL, w(p + "down_b"), w(p + "ls2"), X});
             } else if (stats) {
-                add(DHX_K_RESID_STATS, {r, 1536}, {region(kAct), w(p + "down_w"), w(p + "down_b"), w(p + "ls2"), X, S});
+                add(DHX_K_RESID_STATS, {r, 1536}, {F, w(p + "down_w"), w(p + "down_b"), w(p + "ls2"), X, S});
             } else {
-                add(DHX_K_RESID, {r, 1536}, {region(kAct), w(p + "down_w"), w(p + "down_b"), w(p + "ls2"), X});
+                add(DHX_K_RESID, {r, 1536}, {F, w(p + "down_w"), w(p + "down_b"), w(p + "ls2"), X});
             }
             if (!fused_ln_ && !last) {
-                const std::string n = "l" + std::to_string(i + 1) + "_";
-                add(DHX_K_LAYERNORM, {r}, {X, w(n + "norm1_w"), w(n + "norm1_b"), H});
+                const std::string nx = "l" + std::to_string(i + 1) + "_";
+                add(DHX_K_LAYERNORM, {r}, {X, w(nx + "norm1_w"), w(nx + "norm1_b"), H});
             }
         }
-        add(DHX_K_LAYERNORM_F32, {r}, {X, w("norm_w"), w("norm_b"), region(kOut)});
-        check(dhx_record(engine_.get(), key(b), l.data(), l.size()), engine_.get());
+        add(DHX_K_LAYERNORM_F32, {r}, {X, w("norm_w"), w("norm_b"), O});
+    }
+
+    // Number of image groups run side by side for a batch of b.
+    uint32_t groups(uint64_t b) const {
+        return (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(branches_, b / kMinBranchImages));
     }
 
     // Graph key: batch size plus one bit per plan variant.
     uint64_t key(uint64_t b) const {
-        return b | (splitk_ && b > 1 ? (1ull << 32) : 0) | (fused_ln_ ? 0 : (1ull << 33));
+        return b | (splitk_ && b > 1 ? (1ull << 32) : 0) | (fused_ln_ ? 0 : (1ull << 33)) |
+               ((uint64_t)(groups(b) - 1) << 34);
     }
 
 private:
-    enum { kX, kH, kQ, kK, kVt, kAttn, kAct, kOut, kImage, kPartials, kStats, kBuffers };
+    enum { kX, kH, kQ, kK, kV, kAttn, kAct, kOut, kImage, kPartials, kStats, kBuffers };
     struct EngineFree {
         void operator()(dhx_engine* e) const { dhx_engine_free(e); }
     };
@@ -247,6 +285,7 @@ private:
     uint64_t patches_ = 196, tokens_ = 201, tpad_ = 256, image_elems_ = 0;
     int splitk_ = 0;
     int fused_ln_ = 1;
+    uint32_t branches_ = 2;
     std::unique_ptr<dhx_engine, EngineFree> engine_;
     std::map<std::string, dhx_region> weights_;
     dhx_region a_[kBuffers];
@@ -395,6 +434,10 @@ int dinov3_set_splitk(dinov3_model* m, int mode) {
 
 int dinov3_set_layernorm_fusion(dinov3_model* m, int on) {
     return guarded(m, [&](dhx::Model& x) { x.set_layernorm_fusion(on); });
+}
+
+int dinov3_set_branches(dinov3_model* m, uint32_t n) {
+    return guarded(m, [&](dhx::Model& x) { x.set_branches(n); });
 }
 
 int dinov3_launch_timings(dinov3_model* m, uint64_t images, uint32_t iters, double* ms_out, uint32_t* kernel_out,

@@ -58,6 +58,7 @@ class Region(ctypes.Structure):
 
 MAX_SCALARS = 4  # DHX_MAX_SCALARS
 MAX_BINDINGS = 12  # DHX_MAX_BINDINGS
+MAX_BRANCHES = 4  # DHX_MAX_BRANCHES
 
 
 class Launch(ctypes.Structure):
@@ -93,6 +94,7 @@ def _load_library() -> ctypes.CDLL:
     L.dinov3_replay.argtypes = [vp, c.c_uint64]
     L.dinov3_set_splitk.argtypes = [vp, c.c_int]
     L.dinov3_set_layernorm_fusion.argtypes = [vp, c.c_int]
+    L.dinov3_set_branches.argtypes = [vp, c.c_uint32]
     L.dinov3_launch_timings.argtypes = [vp, c.c_uint64, c.c_uint32, c.POINTER(c.c_double), c.POINTER(c.c_uint32),
                                         c.c_uint64, c.POINTER(c.c_uint64)]
     L.dinov3_write_random_weights.argtypes = [c.c_char_p, c.c_uint64, c.c_int]
@@ -112,6 +114,7 @@ def _load_library() -> ctypes.CDLL:
     L.dhx_weight.argtypes = [vp, vp, c.c_uint64, c.POINTER(Region)]
     L.dhx_upload.argtypes = [vp, Region, vp, c.c_uint64]
     L.dhx_record.argtypes = [vp, c.c_uint64, c.POINTER(Launch), c.c_uint64]
+    L.dhx_record_branches.argtypes = [vp, c.c_uint64, c.POINTER(Launch), c.POINTER(c.c_uint64), c.c_uint32]
     L.dhx_replay.argtypes = [vp, c.c_uint64]
     L.dhx_dispatch.argtypes = [vp, c.c_uint64]
     L.dhx_reserve_readback.argtypes = [vp, c.c_uint64]
@@ -266,6 +269,10 @@ class DINOv3:
         """True (default): LayerNorm folded into the QKV / gate-up GEMMs; False: separate LayerNorm kernels."""
         _check(_lib.dinov3_set_layernorm_fusion(self._h, int(bool(on))), self._h)
 
+    def set_branches(self, n: int) -> None:
+        """Image groups run as concurrent graph branches for batches >= 4*n (default 2)."""
+        _check(_lib.dinov3_set_branches(self._h, int(n)), self._h)
+
     def launch_timings(self, images: int, iters: int = 20) -> list[tuple[str, float]]:
         """Average device ms of each launch of the plan recorded for `images` (HIP events on the model's stream)."""
         cap = 256
@@ -359,8 +366,13 @@ class Engine:
         self._c(_lib.dhx_upload(self._h, region, a.ctypes.data, a.nbytes))
 
     def record(self, key: int, launches: list[tuple[int, list[int], list[Region]]]) -> None:
-        arr = (Launch * len(launches))()
-        for i, (kernel, scalars, bindings) in enumerate(launches):
+        self.record_branches(key, [launches])
+
+    def record_branches(self, key: int, branches: list[list[tuple[int, list[int], list[Region]]]]) -> None:
+        """Record launch lists that may run concurrently (each list in order) as one graph."""
+        flat = [l for b in branches for l in b]
+        arr = (Launch * max(1, len(flat)))()
+        for i, (kernel, scalars, bindings) in enumerate(flat):
             if len(scalars) > MAX_SCALARS or len(bindings) > MAX_BINDINGS:
                 raise ValueError("too many scalars or bindings for one launch")
             arr[i].kernel = kernel
@@ -369,7 +381,8 @@ class Engine:
             arr[i].n_bindings = len(bindings)
             for j, b in enumerate(bindings):
                 arr[i].bindings[j] = b
-        self._c(_lib.dhx_record(self._h, int(key), arr, len(launches)))
+        counts = (ctypes.c_uint64 * max(1, len(branches)))(*[len(b) for b in branches])
+        self._c(_lib.dhx_record_branches(self._h, int(key), arr, counts, len(branches)))
 
     def replay(self, key: int) -> None:
         self._c(_lib.dhx_replay(self._h, int(key)))

@@ -97,6 +97,12 @@ int dinov3_set_splitk(dinov3_model *m, int mode);
  * 0 runs separate LayerNorm kernels as the reference does (86 launches).
  * Graphs are kept per (batch, variant). */
 int dinov3_set_layernorm_fusion(dinov3_model *m, int on);
+/* Image groups run side by side (no reference counterpart): batches of at
+ * least 4*n images are cut into n groups (1 <= n <= DHX_MAX_BRANCHES,
+ * default 2) recorded as concurrent branches of one graph, so one group's
+ * kernels fill the last partial wave of workgroups of the other's. Results
+ * are bitwise the same for every n. Graphs are kept per (batch, variant). */
+int dinov3_set_branches(dinov3_model *m, uint32_t n);
 /* dhx_launch_timings for the plan the model would replay for `images`. */
 int dinov3_launch_timings(dinov3_model *m, uint64_t images, uint32_t iters, double *ms_out, uint32_t *kernel_out,
                           uint64_t capacity, uint64_t *count);

@@ -84,6 +84,7 @@ enum {
 
 #define DHX_MAX_SCALARS 4
 #define DHX_MAX_BINDINGS 12
+#define DHX_MAX_BRANCHES 4
 
 /* One dispatch; replaces engine.rs:21-27 `Launch`. The grid is derived from
  * the scalars by each kernel's launcher. */
@@ -123,6 +124,16 @@ int dhx_upload(dhx_engine *e, dhx_region r, const void *bytes, uint64_t n);
  * hipGraph for `batch` and keep it with its launch list. Recording a batch
  * that already has a graph is a no-op. */
 int dhx_record(dhx_engine *e, uint64_t batch, const dhx_launch *launches, uint64_t n);
+/* dhx_record for a plan made of independent chains (no counterpart in the
+ * reference, whose graph is one chain): launches holds `branches` lists back
+ * to back, counts[i] launches each (1 <= branches <= DHX_MAX_BRANCHES). Each
+ * list runs in order; different lists may run concurrently (on forked
+ * streams inside the graph, and likewise for dhx_dispatch / dhx_benchmark),
+ * so they must not write memory another list reads or writes. The model
+ * uses this to run halves of a batch side by side, filling the last partial
+ * wave of one half's kernels with the other half's work. */
+int dhx_record_branches(dhx_engine *e, uint64_t batch, const dhx_launch *launches, const uint64_t *counts,
+                        uint32_t branches);
 int dhx_has_graph(const dhx_engine *e, uint64_t batch);
 /* engine.rs:203-214 (replay): launch the graph recorded for `batch`. */
 int dhx_replay(dhx_engine *e, uint64_t batch);

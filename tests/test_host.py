@@ -37,6 +37,7 @@ def test_binding_structs_match_header(tmp_path):
     text = open(os.path.join(ROOT, "include", "dinov3_engine.h")).read()
     consts = dict(re.findall(r"#define (DHX_MAX_\w+) (\d+)", text))
     assert int(consts["DHX_MAX_SCALARS"]) == d.MAX_SCALARS and int(consts["DHX_MAX_BINDINGS"]) == d.MAX_BINDINGS
+    assert int(consts["DHX_MAX_BRANCHES"]) == d.MAX_BRANCHES
     enum = dict((n, int(v)) for n, v in re.findall(r"(DHX_K_\w+) = (\d+)", text))
     assert [n[6:].lower() for n, _ in sorted(enum.items(), key=lambda kv: kv[1])] == d.KERNELS
     # the struct layouts the C compiler gives the header

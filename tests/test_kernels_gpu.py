@@ -76,6 +76,36 @@ def test_allocation_fill_is_ordered_before_upload(eng):
         assert np.array_equal(eng.read(r, np.uint8, a.shape), a)
 
 
+def test_record_branches(eng):
+    # Two independent chains recorded as concurrent branches of one graph
+    # (and dispatched directly) give the results of running each alone.
+    rng = np.random.default_rng(5)
+    xs = [f16(rng.normal(size=(3000, 384))) for _ in range(3)]
+    g = rng.normal(size=384).astype(np.float32)
+    b = rng.normal(size=384).astype(np.float32)
+    G, B = up(eng, g), up(eng, b)
+    ins = [up(eng, x) for x in xs]
+    mid = [eng.allocate(3000 * 384 * 2) for _ in xs]
+    outs = [eng.allocate(3000 * 384 * 4) for _ in xs]
+    branches = [[(K_LN, [3000], [ins[i], G, B, mid[i]]), (K_LN32, [3000], [mid[i], G, B, outs[i]])] for i in range(3)]
+    key = next(_keys)
+    eng.record_branches(key, branches)
+    eng.replay(key)
+    eng.synchronize()
+    want = [eng.read(o, np.float32, (3000, 384)).copy() for o in outs]
+    for i, x in enumerate(xs):
+        ref = oracle.layernorm(oracle.round_f16(oracle.layernorm(x.astype(np.float64), g, b)), g, b)
+        check(want[i], ref, atol=2e-3, rel=2e-3, what=f"branch {i}")
+    for o in outs:
+        eng.upload(o, np.zeros((3000, 384), np.float32))
+    eng.dispatch(key)
+    eng.synchronize()
+    for i, o in enumerate(outs):
+        assert np.array_equal(eng.read(o, np.float32, (3000, 384)), want[i])
+    with pytest.raises(d.DINOv3Error, match="branches must be 1..4"):
+        eng.record_branches(next(_keys), [branches[0]] * 5)
+
+
 @pytest.mark.parametrize("rows", [1, 1001, 12864])
 @pytest.mark.parametrize("f32_out", [False, True])
 def test_layernorm(eng, rows, f32_out):

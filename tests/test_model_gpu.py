@@ -133,6 +133,28 @@ def test_layernorm_fusion_matches_unfused_plan(models, oracle_weights, preset):
     compare(fused[0], want, f"fused plan preset {preset}")
 
 
+def test_branches_are_bitwise_identical(models):
+    # Image groups recorded as concurrent graph branches: every grouping gives
+    # the same bits (a row's arithmetic never depends on its group), in both
+    # graph replay and the direct-dispatch path used by benchmark().
+    m = models(1, max_batch=16)
+    px = d.random_pixels(8, 16)
+    m.set_branches(1)
+    try:
+        base = m.forward(px)
+        for n in (2, 3, 4):
+            m.set_branches(n)
+            assert np.array_equal(m.forward(px), base), f"{n} branches"
+            assert np.array_equal(m.forward(px[:9]), base[:9]), f"{n} branches, 9 images"
+        t = m.benchmark(px, 10)
+        assert t.samples == 10
+        assert np.array_equal(m.forward(px), base)
+        with pytest.raises(d.DINOv3Error, match="branches must be 1..4"):
+            m.set_branches(5)
+    finally:
+        m.set_branches(2)
+
+
 def test_splitk_variant(models):
     m = models(1, max_batch=8)
     px = d.random_pixels(5, 8)
