@@ -14,7 +14,9 @@
 // Lane l holds query (l % 32) and 16 of every 32 keys; the other 16 are in
 // lane l ^ 32, so each row max / row sum is 15 in-register ops plus one
 // cross-half exchange, and the running rescale of O^T is a per-lane scalar.
-// The score scale 1/8 is folded with log2(e) so the softmax uses v_exp_f32.
+// Q is scaled by 1/8 in registers and log2(e) is folded into one FMA per
+// score, so the softmax runs on v_exp_f32; the running max is updated lazily
+// (only when it grows by more than kLazy), which skips most rescales of O.
 // P is rounded to f16 for the PV product; the denominator keeps the fp32
 // weights (as in the reference, attention_online_f16_wmma_cf16.loom:195-216).
 #include "launch.hpp"
@@ -26,6 +28,7 @@ constexpr int kThreads = 256;
 constexpr int KB = 64;    // keys per LDS block
 constexpr int KLD = 72;   // LDS row pitch in halfs
 constexpr int QB = 128;   // queries per workgroup
+constexpr float kLazy = 8.0f;  // running-max slack of the lazy rescaling (score units)
 
 __device__ __forceinline__ half8_t zero8() {
     half8_t z = {};
@@ -80,11 +83,17 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttentionArgs p) {
     // 16*(group%2) + j of four consecutive keys.
     const int tr_row = (lane & 15) >> 2, tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
-    const float scale = 0.125f * kLog2e;
+    // Scores are s = (q / 8) . k: Q is scaled by 1/8 once (a power of two,
+    // exact for normal f16 values), and the softmax weight of a score is
+    // 2^(s*log2e - m*log2e), one FMA and one v_exp_f32.
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) qf[kk] *= (half_t)0.125f;
     const float neg_inf = -__builtin_inff();
     float16_t o[2] = {float16_t{}, float16_t{}};
     float m_run = -1e30f, l_run = 0.f;
     const int nkb = (T + KB - 1) / KB;
+    // Waves whose 32 queries all lie past T only help move K and V.
+    const bool active = qb * QB + wave * 32 < T;
 
     load(0);
     store(0);
@@ -94,7 +103,7 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttentionArgs p) {
         const bool more = kb + 1 < nkb;
         if (more) load(kb + 1);
 #pragma unroll
-        for (int sub = 0; sub < 2; ++sub) {
+        for (int sub = 0; sub < 2 && active; ++sub) {
             const int key0 = kb * KB + sub * 32;
             if (key0 >= T) break;  // uniform across the workgroup
             float16_t s = {};
@@ -102,27 +111,36 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttentionArgs p) {
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) s = mfma32x32x16(*(const half8_t*)(krow + kk * 16), qf[kk], s);
             // s[r] is the score of key key0 + 8(r/4) + 4*hi + r%4 for query l32.
-            float mx = neg_inf;
+            if (key0 + 32 > T) {  // the last, partial block of keys (uniform)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int key = key0 + 8 * (r >> 2) + 4 * hi + (r & 3);
-                s[r] = key < T ? s[r] * scale : neg_inf;
-                mx = fmaxf(mx, s[r]);
+                for (int r = 0; r < 16; ++r)
+                    if (key0 + 8 * (r >> 2) + 4 * hi + (r & 3) >= T) s[r] = neg_inf;
             }
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const float m_new = fmaxf(m_run, mx);
-            const float alpha = fast_exp2(m_run - m_new);
+            float mx = s[0];
+#pragma unroll
+            for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));  // every sub-block holds a valid key of each pair
+            // Lazy rescaling: the running max moves only when a score exceeds
+            // it by more than kLazy, so weights stay below e^kLazy (well inside
+            // f16 for P) and most sub-blocks skip rescaling O entirely.
+            const bool grow = mx > m_run + kLazy;
+            if (__any(grow)) {  // uniform across the wave
+                const float m_new = grow ? mx : m_run;
+                const float alpha = fast_exp2((m_run - m_new) * kLog2e);
+                l_run *= alpha;
+                o[0] *= alpha;
+                o[1] *= alpha;
+                m_run = m_new;
+            }
+            const float mb = m_run * kLog2e;
             float sum = 0.f;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                s[r] = fast_exp2(s[r] - m_new);
+                s[r] = fast_exp2(fmaf(s[r], kLog2e, -mb));
                 sum += s[r];
             }
             sum += __shfl_xor(sum, 32, 64);
-            l_run = l_run * alpha + sum;
-            m_run = m_new;
-            o[0] *= alpha;
-            o[1] *= alpha;
+            l_run += sum;
             // P^T as the b operand: k-slice element j of this lane is key
             // key0 + 16ks + (j < 4 ? 4hi + j : 8 + 4hi + j - 4); the V^T
             // transpose reads below give channel ct*32 + l32 of the same keys.

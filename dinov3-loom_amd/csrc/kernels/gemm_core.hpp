@@ -2,9 +2,9 @@
 // accumulation, shared by every GEMM variant of the forward pass.
 //
 // A workgroup of WGM x WGN waves owns a BM x BN output tile; the K loop walks
-// 64-wide stages. Stages move HBM/L2 -> registers -> LDS with two register
-// sets and two LDS buffers, so the global loads of stage s+2 are in flight
-// while stage s feeds the MFMAs and stage s+1 is written to LDS. The LDS
+// BK-wide stages (64 or 32). Stages move HBM/L2 -> registers -> LDS with two
+// register sets and two LDS buffers, so the global loads of stage s+2 are in
+// flight while stage s feeds the MFMAs and stage s+1 is written to LDS. The LDS
 // barrier only waits for LDS traffic (s_waitcnt lgkmcnt(0); s_barrier):
 // __syncthreads() would also drain every outstanding global load (its
 // workgroup release fence waits on vmcnt(0)) and serialise the pipeline.
@@ -25,12 +25,14 @@
 namespace dhx {
 namespace gemm {
 
-constexpr int BK = 64;
-constexpr int LDK = BK + 8;  // LDS row pitch in halfs (144 B): conflict-free 16-byte fragment reads
-
-template <int BM_, int BN_, int WGM_, int WGN_>
+template <int BM_, int BN_, int WGM_, int WGN_, int BK_ = 64>
 struct Tile {
     static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_;
+    static constexpr int BK = BK_;
+    // LDS row pitch in halfs (144 B for BK 64, 80 B for BK 32): the 16-byte
+    // fragment reads of 8 consecutive rows hit disjoint banks.
+    static constexpr int LDK = BK + 8;
+    static_assert(BK == 64 || BK == 32, "stage depth");
     static constexpr int WAVES = WGM * WGN, THREADS = 64 * WAVES;
     static constexpr int TM = BM / WGM, TN = BN / WGN;
     static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile is a multiple of the 32x32 MFMA tile");
@@ -55,15 +57,23 @@ __device__ __forceinline__ half8_t zero8() {
 // output rows that are never stored, and an unconditional load keeps the
 // compiler's vmcnt accounting exact (a predicated load makes every later wait
 // drain the prefetches too).
-template <int ROWS, int THREADS>
+template <int ROWS, int THREADS, int BK, int LDK>
 struct HalfTile {
-    static constexpr int CHUNKS = ROWS * BK / 8 / THREADS;
-    static_assert(ROWS * BK / 8 % THREADS == 0, "tile splits evenly over the workgroup");
+    // 16-byte chunks of one stage; when they do not split evenly over the
+    // workgroup, the surplus threads repeat the last chunk (same data to the
+    // same LDS location), which keeps every load unconditional.
+    static constexpr int CPR = BK / 8;  // chunks per row
+    static constexpr int TOTAL = ROWS * CPR;
+    static constexpr int CHUNKS = (TOTAL + THREADS - 1) / THREADS;
     half8_t r[CHUNKS];
+    __device__ __forceinline__ static int chunk(int tid, int i) {
+        const int c = tid + i * THREADS;
+        return TOTAL % THREADS == 0 ? c : min(c, TOTAL - 1);
+    }
     __device__ __forceinline__ void load(const half_t* base, int ld, int r0, int limit, int k0, int tid) {
 #pragma unroll
         for (int i = 0; i < CHUNKS; ++i) {
-            const int c = tid + i * THREADS, row = c >> 3, col = (c & 7) * 8;
+            const int c = chunk(tid, i), row = c / CPR, col = (c % CPR) * 8;
             const int m = min(r0 + row, limit - 1);
             r[i] = *(const half8_t*)(base + (size_t)m * ld + k0 + col);
         }
@@ -71,14 +81,14 @@ struct HalfTile {
     __device__ __forceinline__ void load_all(const half_t* base, int ld, int r0, int k0, int tid) {
 #pragma unroll
         for (int i = 0; i < CHUNKS; ++i) {
-            const int c = tid + i * THREADS, row = c >> 3, col = (c & 7) * 8;
+            const int c = chunk(tid, i), row = c / CPR, col = (c % CPR) * 8;
             r[i] = *(const half8_t*)(base + (size_t)(r0 + row) * ld + k0 + col);
         }
     }
     __device__ __forceinline__ void store(half_t* s, int tid) const {
 #pragma unroll
         for (int i = 0; i < CHUNKS; ++i) {
-            const int c = tid + i * THREADS, row = c >> 3, col = (c & 7) * 8;
+            const int c = chunk(tid, i), row = c / CPR, col = (c % CPR) * 8;
             *(half8_t*)(s + row * LDK + col) = r[i];
         }
     }
@@ -87,11 +97,11 @@ struct HalfTile {
 // A operand: f16 activations [M][lda], rows m0 .. m0+BM-1.
 template <class T>
 struct ActRows {
-    HalfTile<T::BM, T::THREADS> t;
+    HalfTile<T::BM, T::THREADS, T::BK, T::LDK> t;
     const half_t* a;
     int lda, M, k_off;
     __device__ __forceinline__ void load(int m0, int /*n0*/, int kt, int tid) {
-        t.load(a, lda, m0, M, k_off + kt * BK, tid);
+        t.load(a, lda, m0, M, k_off + kt * T::BK, tid);
     }
     __device__ __forceinline__ void store(half_t* s, int tid) const { t.store(s, tid); }
 };
@@ -100,11 +110,11 @@ struct ActRows {
 // that are multiples of BN, so every row exists).
 template <class T>
 struct WeightRows {
-    HalfTile<T::BN, T::THREADS> t;
+    HalfTile<T::BN, T::THREADS, T::BK, T::LDK> t;
     const half_t* w;
     int ldw, k_off;
     __device__ __forceinline__ void load(int /*m0*/, int n0, int kt, int tid) {
-        t.load_all(w, ldw, n0, k_off + kt * BK, tid);
+        t.load_all(w, ldw, n0, k_off + kt * T::BK, tid);
     }
     __device__ __forceinline__ void store(half_t* s, int tid) const { t.store(s, tid); }
 };
@@ -114,7 +124,7 @@ struct Acc {
     float16_t v[T::FN][T::FM];
 };
 
-// One 64-deep stage of MFMAs from LDS. Fragments are double-buffered in
+// One BK-deep stage of MFMAs from LDS. Fragments are double-buffered in
 // registers: the reads for k-slice kk+1 are issued before the MFMAs of kk, so
 // LDS latency overlaps the matrix pipe instead of stalling each MFMA.
 template <class T>
@@ -122,19 +132,19 @@ __device__ __forceinline__ void mma_stage(const half_t* stage, int tid, Acc<T>& 
     const int lane = tid & 63, wave = tid >> 6;
     const int wm = wave % T::WGM, wn = wave / T::WGM;
     const int l32 = lane & 31, hi = lane >> 5;
-    const half_t* a_s = stage + (wm * T::TM + l32) * LDK + hi * 8;
-    const half_t* w_s = stage + (T::BM + wn * T::TN + l32) * LDK + hi * 8;
+    const half_t* a_s = stage + (wm * T::TM + l32) * T::LDK + hi * 8;
+    const half_t* w_s = stage + (T::BM + wn * T::TN + l32) * T::LDK + hi * 8;
     half8_t wf[2][T::FN], af[2][T::FM];
     auto fetch = [&](int kk, int b) {
 #pragma unroll
-        for (int i = 0; i < T::FN; ++i) wf[b][i] = *(const half8_t*)(w_s + i * 32 * LDK + kk * 16);
+        for (int i = 0; i < T::FN; ++i) wf[b][i] = *(const half8_t*)(w_s + i * 32 * T::LDK + kk * 16);
 #pragma unroll
-        for (int j = 0; j < T::FM; ++j) af[b][j] = *(const half8_t*)(a_s + j * 32 * LDK + kk * 16);
+        for (int j = 0; j < T::FM; ++j) af[b][j] = *(const half8_t*)(a_s + j * 32 * T::LDK + kk * 16);
     };
     fetch(0, 0);
 #pragma unroll
-    for (int kk = 0; kk < BK / 16; ++kk) {
-        if (kk + 1 < BK / 16) fetch(kk + 1, (kk + 1) & 1);
+    for (int kk = 0; kk < T::BK / 16; ++kk) {
+        if (kk + 1 < T::BK / 16) fetch(kk + 1, (kk + 1) & 1);
 #pragma unroll
         for (int i = 0; i < T::FN; ++i)
 #pragma unroll
@@ -155,7 +165,7 @@ __device__ __forceinline__ int xcd_tile(int total) {
 }
 
 // The pipelined K loop of one tile; k_tiles must be even (host-checked:
-// K % 128 == 0). The loaders take the tile origin (m0, n0) and the stage.
+// K % 128 == 0, so K / BK is even for BK 64 and 32). The loaders take the tile origin (m0, n0) and the stage.
 template <class T, class AL, class WL>
 __device__ __forceinline__ void gemm_main(AL (&al)[2], WL (&wl)[2], int m0, int n0, int k_tiles, half_t* lds,
                                           Acc<T>& acc) {
@@ -172,7 +182,7 @@ __device__ __forceinline__ void gemm_main(AL (&al)[2], WL (&wl)[2], int m0, int 
     al[1].load(m0, n0, min(1, last), tid);
     wl[1].load(m0, n0, min(1, last), tid);
     al[0].store(s0, tid);
-    wl[0].store(s0 + T::BM * LDK, tid);
+    wl[0].store(s0 + T::BM * T::LDK, tid);
     lds_barrier();
     for (int kt = 0; kt < k_tiles; kt += 2) {
         // s0 holds stage kt; register set 1 holds stage kt+1 (maybe in flight).
@@ -180,14 +190,14 @@ __device__ __forceinline__ void gemm_main(AL (&al)[2], WL (&wl)[2], int m0, int 
         wl[0].load(m0, n0, min(kt + 2, last), tid);
         mma_stage<T>(s0, tid, acc);
         al[1].store(s1, tid);
-        wl[1].store(s1 + T::BM * LDK, tid);
+        wl[1].store(s1 + T::BM * T::LDK, tid);
         lds_barrier();
         al[1].load(m0, n0, min(kt + 3, last), tid);
         wl[1].load(m0, n0, min(kt + 3, last), tid);
         mma_stage<T>(s1, tid, acc);
         if (kt + 2 < k_tiles) {
             al[0].store(s0, tid);
-            wl[0].store(s0 + T::BM * LDK, tid);
+            wl[0].store(s0 + T::BM * T::LDK, tid);
         }
         lds_barrier();
     }

@@ -19,8 +19,9 @@ namespace gemm {
 // on the way to LDS.
 template <class T>
 struct PatchRows {
-    static constexpr int CHUNKS = T::BM * BK / 4 / T::THREADS;
-    static_assert(T::BM * BK / 4 % T::THREADS == 0, "patch tile splits evenly");
+    static_assert(T::BK == 64, "a stage is one channel x four pixel rows");
+    static constexpr int CHUNKS = T::BM * T::BK / 4 / T::THREADS;
+    static_assert(T::BM * T::BK / 4 % T::THREADS == 0, "patch tile splits evenly");
     const float* px;
     int M, G, P, S;
     float4_t r[CHUNKS];
@@ -40,7 +41,7 @@ struct PatchRows {
         for (int i = 0; i < CHUNKS; ++i) {
             const int c = tid + i * T::THREADS;
             const int dxq = c & 3, row = (c >> 2) % T::BM, dyl = c / (4 * T::BM);
-            *(half4_t*)(s + row * LDK + dyl * 16 + dxq * 4) = to_half4(r[i]);
+            *(half4_t*)(s + row * T::LDK + dyl * 16 + dxq * 4) = to_half4(r[i]);
         }
     }
 };
@@ -80,7 +81,7 @@ __global__ __launch_bounds__(T::THREADS) void patch_embed_kernel(PatchEmbedArgs 
     const int S = 16 * p.grid;
     PatchRows<T> al[2] = {{p.pixels, M, p.grid, P, S}, {p.pixels, M, p.grid, P, S}};
     WeightRows<T> wl[2] = {{{}, p.w, 768, 0}, {{}, p.w, 768, 0}};
-    gemm_tile<T>(al, wl, NT, NT * ((M + T::BM - 1) / T::BM), 768 / BK, lds, [&](const Acc<T>& acc, int m0, int n0) {
+    gemm_tile<T>(al, wl, NT, NT * ((M + T::BM - 1) / T::BM), 768 / T::BK, lds, [&](const Acc<T>& acc, int m0, int n0) {
         const Frag<T> f(m0, n0);
         half_t* const st = lds + (threadIdx.x >> 6) * (T::TM * SP);
 #pragma unroll
@@ -146,7 +147,7 @@ __global__ __launch_bounds__(T::THREADS) void qkv_rope_kernel(QkvArgs p) {
     constexpr int NT = 3 * kHidden / T::BN;
     ActRows<T> al[2] = {{{}, p.h, kHidden, M, 0}, {{}, p.h, kHidden, M, 0}};
     WeightRows<T> wl[2] = {{{}, p.w, kHidden, 0}, {{}, p.w, kHidden, 0}};
-    gemm_tile<T>(al, wl, NT, NT * ((M + T::BM - 1) / T::BM), kHidden / BK, lds, [&](const Acc<T>& acc, int m0, int n0) {
+    gemm_tile<T>(al, wl, NT, NT * ((M + T::BM - 1) / T::BM), kHidden / T::BK, lds, [&](const Acc<T>& acc, int m0, int n0) {
         const Frag<T> f(m0, n0);
         const int lane = threadIdx.x & 63;
         half_t* const st = lds + (threadIdx.x >> 6) * (T::TM * SP);
@@ -225,7 +226,7 @@ __global__ __launch_bounds__(T::THREADS) void resid_kernel(ResidArgs p) {
     constexpr int NT = kHidden / T::BN;
     ActRows<T> al[2] = {{{}, p.a, p.k, p.rows, 0}, {{}, p.a, p.k, p.rows, 0}};
     WeightRows<T> wl[2] = {{{}, p.w, p.k, 0}, {{}, p.w, p.k, 0}};
-    gemm_tile<T>(al, wl, NT, NT * ((p.rows + T::BM - 1) / T::BM), p.k / BK, lds,
+    gemm_tile<T>(al, wl, NT, NT * ((p.rows + T::BM - 1) / T::BM), p.k / T::BK, lds,
                        [&](const Acc<T>& acc, int m0, int n0) {
         const Frag<T> f(m0, n0);
         float* const st = reinterpret_cast<float*>(lds) + (threadIdx.x >> 6) * (T::TM * SPF);
@@ -280,35 +281,37 @@ __global__ __launch_bounds__(T::THREADS) void swiglu_kernel(SwigluArgs p) {
     constexpr int NT = 2 * kFF / T::BN;
     ActRows<T> al[2] = {{{}, p.h, kHidden, p.rows, 0}, {{}, p.h, kHidden, p.rows, 0}};
     WeightRows<T> wl[2] = {{{}, p.w, kHidden, 0}, {{}, p.w, kHidden, 0}};
-    gemm_tile<T>(al, wl, NT, NT * ((p.rows + T::BM - 1) / T::BM), kHidden / BK, lds,
+    gemm_tile<T>(al, wl, NT, NT * ((p.rows + T::BM - 1) / T::BM), kHidden / T::BK, lds,
                        [&](const Acc<T>& acc, int m0, int n0) {
         const Frag<T> f(m0, n0);
         const int wave = threadIdx.x >> 6;
         half_t* const st = lds + (wave % T::WGM) * T::TM * SP + (wave / T::WGM) * 32;
-        float4_t bias[2][4], wsum[2][4];
+        RowNorm rn[T::FM];
+#pragma unroll
+        for (int j = 0; j < T::FM; ++j) {
+            rn[j] = RowNorm{0.f, 1.f};
+            if constexpr (LN) rn[j] = row_norm(p.stats, min(f.row(j), p.rows - 1));
+        }
+        // Column constants are loaded per register group (not all at once)
+        // to keep the epilogue's register footprint small next to acc.
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const int c = g * 8 + f.hi * 4;
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                bias[i][g] = ld4(p.bias + f.n_base + 32 * i + c);
-                if constexpr (LN) wsum[i][g] = ld4(p.wsum + f.n_base + 32 * i + c);
+            const float4_t bg = ld4(p.bias + f.n_base + c), bu = ld4(p.bias + f.n_base + 32 + c);
+            float4_t wg{}, wu{};
+            if constexpr (LN) {
+                wg = ld4(p.wsum + f.n_base + c);
+                wu = ld4(p.wsum + f.n_base + 32 + c);
             }
-        }
 #pragma unroll
-        for (int j = 0; j < T::FM; ++j) {
-            RowNorm rn{0.f, 1.f};
-            if constexpr (LN) rn = row_norm(p.stats, min(f.row(j), p.rows - 1));
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int c = g * 8 + f.hi * 4;
+            for (int j = 0; j < T::FM; ++j) {
                 float4_t gate = group4(acc.v[0][j], g), up = group4(acc.v[1][j], g);
                 if constexpr (LN) {
-                    gate = (gate - rn.mean * wsum[0][g]) * rn.rstd;
-                    up = (up - rn.mean * wsum[1][g]) * rn.rstd;
+                    gate = (gate - rn[j].mean * wg) * rn[j].rstd;
+                    up = (up - rn[j].mean * wu) * rn[j].rstd;
                 }
-                gate += bias[0][g];
-                up += bias[1][g];
+                gate += bg;
+                up += bu;
                 const float4_t y = float4_t{silu(gate[0]), silu(gate[1]), silu(gate[2]), silu(gate[3])} * up;
                 *(half4_t*)(st + (j * 32 + f.l32) * SP + c) = to_half4(y);
             }
@@ -364,7 +367,7 @@ __global__ __launch_bounds__(T::THREADS) void splitk_kernel(SplitKArgs p) {
     const SplitDecode<T> d{MT, p.k / p.splits};
     SplitActRows<T> al[2] = {{{{}, p.a, p.k, p.rows, 0}, d}, {{{}, p.a, p.k, p.rows, 0}, d}};
     SplitWeightRows<T> wl[2] = {{{{}, p.w, p.k, 0}, d}, {{{}, p.w, p.k, 0}, d}};
-    gemm_tile<T>(al, wl, NT, NT * MT * p.splits, d.kc / BK, lds, [&](const Acc<T>& acc, int m0, int n0) {
+    gemm_tile<T>(al, wl, NT, NT * MT * p.splits, d.kc / T::BK, lds, [&](const Acc<T>& acc, int m0, int n0) {
         const Frag<T> f(d.row0(m0), n0);
         float* slab = p.partials + (size_t)d.split(m0) * p.rows * kHidden;
 #pragma unroll
