@@ -162,12 +162,33 @@ __global__ __launch_bounds__(T::THREADS) void qkv_rope_kernel(QkvArgs p) {
                 if constexpr (LN) wsum[i][g] = ld4(p.wsum + f.n_base + 32 * i + c);
             }
         }
+        const bool rope_part = part < 2;  // uniform per wave
 #pragma unroll
         for (int j = 0; j < T::FM; ++j) {
             const int m = min(f.row(j), M - 1);  // rows past M are computed but never written out
             const int tok = m % Tok;
-            const bool rotate = part < 2 && tok >= kPrefix;
+            // RoPE angles of this row, loaded together before any use (lanes
+            // hold different rows, so each load is a gather; one round trip
+            // per row instead of one per register group). Prefix rows and v
+            // columns rotate by cos 1, sin 0.
             const size_t angle_row = (size_t)max(tok - kPrefix, 0) * kHeadDim;
+            float4_t co[4], si[4];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                co[g] = float4_t{1.f, 1.f, 1.f, 1.f};
+                si[g] = float4_t{};
+                if (rope_part) {
+                    co[g] = ld4(p.cos + angle_row + g * 8 + f.hi * 4);
+                    si[g] = ld4(p.sin + angle_row + g * 8 + f.hi * 4);
+                }
+            }
+            if (tok < kPrefix) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    co[g] = float4_t{1.f, 1.f, 1.f, 1.f};
+                    si[g] = float4_t{};
+                }
+            }
             RowNorm rn{0.f, 1.f};
             if constexpr (LN) rn = row_norm(p.stats, m);
             half_t* const row = st + (j * 32 + f.l32) * SP;
@@ -181,15 +202,10 @@ __global__ __launch_bounds__(T::THREADS) void qkv_rope_kernel(QkvArgs p) {
                 }
                 lo += bias[0][g];
                 up += bias[1][g];
-                if (rotate) {
-                    const float4_t co = ld4(p.cos + angle_row + c), si = ld4(p.sin + angle_row + c);
-                    const float4_t nlo = lo * co - up * si;  // x[c] cos - x[c+32] sin
-                    const float4_t nup = up * co + lo * si;  // x[c+32] cos + x[c] sin
-                    lo = nlo;
-                    up = nup;
-                }
-                *(half4_t*)(row + c) = to_half4(lo);
-                *(half4_t*)(row + 32 + c) = to_half4(up);
+                const float4_t nlo = lo * co[g] - up * si[g];  // x[c] cos - x[c+32] sin
+                const float4_t nup = up * co[g] + lo * si[g];  // x[c+32] cos + x[c] sin
+                *(half4_t*)(row + c) = to_half4(nlo);
+                *(half4_t*)(row + 32 + c) = to_half4(nup);
             }
         }
         wave_lds_sync();
