@@ -270,7 +270,7 @@ class DINOv3:
         _check(_lib.dinov3_set_layernorm_fusion(self._h, int(bool(on))), self._h)
 
     def set_branches(self, n: int) -> None:
-        """Image groups run as concurrent graph branches for batches >= 4*n (default 2)."""
+        """Image groups run as concurrent graph branches for batches >= 4*n (default 3)."""
         _check(_lib.dinov3_set_branches(self._h, int(n)), self._h)
 
     def launch_timings(self, images: int, iters: int = 20) -> list[tuple[str, float]]:

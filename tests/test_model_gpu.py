@@ -152,7 +152,7 @@ def test_branches_are_bitwise_identical(models):
         with pytest.raises(d.DINOv3Error, match="branches must be 1..4"):
             m.set_branches(5)
     finally:
-        m.set_branches(2)
+        m.set_branches(3)
 
 
 def test_splitk_variant(models):
