@@ -288,7 +288,7 @@ __global__ __launch_bounds__(T::THREADS) void resid_kernel(ResidArgs p) {
 // staged in LDS and written as whole row pieces of BN bytes.
 template <class T, bool LN>
 __global__ __launch_bounds__(T::THREADS) void swiglu_kernel(SwigluArgs p) {
-    static_assert(T::TN == 64, "gate/up pair per wave");
+    static_assert(T::TN % 64 == 0, "whole gate/up pairs per wave");
     constexpr int OW = T::BN / 2;   // act columns per workgroup
     constexpr int SP = OW + 8;      // staging pitch in halfs
     constexpr int LPR = OW / 8;     // lanes per row in the copy-out
@@ -301,37 +301,40 @@ __global__ __launch_bounds__(T::THREADS) void swiglu_kernel(SwigluArgs p) {
                        [&](const Acc<T>& acc, int m0, int n0) {
         const Frag<T> f(m0, n0);
         const int wave = threadIdx.x >> 6;
-        half_t* const st = lds + (wave % T::WGM) * T::TM * SP + (wave / T::WGM) * 32;
+        half_t* const st = lds + (wave % T::WGM) * T::TM * SP + (wave / T::WGM) * (T::TN / 2);
         RowNorm rn[T::FM];
 #pragma unroll
         for (int j = 0; j < T::FM; ++j) {
             rn[j] = RowNorm{0.f, 1.f};
             if constexpr (LN) rn[j] = row_norm(p.stats, min(f.row(j), p.rows - 1));
         }
-        // Column constants are loaded per register group (not all at once)
-        // to keep the epilogue's register footprint small next to acc.
+        // Pair q of the wave: gate = acc.v[2q], up = acc.v[2q + 1], outputs
+        // 32q .. 32q+31 of the wave's TN/2. Column constants are loaded per
+        // register group to keep the register footprint small next to acc.
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const int c = g * 8 + f.hi * 4;
-            const float4_t bg = ld4(p.bias + f.n_base + c), bu = ld4(p.bias + f.n_base + 32 + c);
-            float4_t wg{}, wu{};
-            if constexpr (LN) {
-                wg = ld4(p.wsum + f.n_base + c);
-                wu = ld4(p.wsum + f.n_base + 32 + c);
-            }
+        for (int q = 0; q < T::FN / 2; ++q)
 #pragma unroll
-            for (int j = 0; j < T::FM; ++j) {
-                float4_t gate = group4(acc.v[0][j], g), up = group4(acc.v[1][j], g);
+            for (int g = 0; g < 4; ++g) {
+                const int c = g * 8 + f.hi * 4, n = f.n_base + 64 * q + c;
+                const float4_t bg = ld4(p.bias + n), bu = ld4(p.bias + n + 32);
+                float4_t wg{}, wu{};
                 if constexpr (LN) {
-                    gate = (gate - rn[j].mean * wg) * rn[j].rstd;
-                    up = (up - rn[j].mean * wu) * rn[j].rstd;
+                    wg = ld4(p.wsum + n);
+                    wu = ld4(p.wsum + n + 32);
                 }
-                gate += bg;
-                up += bu;
-                const float4_t y = float4_t{silu(gate[0]), silu(gate[1]), silu(gate[2]), silu(gate[3])} * up;
-                *(half4_t*)(st + (j * 32 + f.l32) * SP + c) = to_half4(y);
+#pragma unroll
+                for (int j = 0; j < T::FM; ++j) {
+                    float4_t gate = group4(acc.v[2 * q][j], g), up = group4(acc.v[2 * q + 1][j], g);
+                    if constexpr (LN) {
+                        gate = (gate - rn[j].mean * wg) * rn[j].rstd;
+                        up = (up - rn[j].mean * wu) * rn[j].rstd;
+                    }
+                    gate += bg;
+                    up += bu;
+                    const float4_t y = float4_t{silu(gate[0]), silu(gate[1]), silu(gate[2]), silu(gate[3])} * up;
+                    *(half4_t*)(st + (j * 32 + f.l32) * SP + 32 * q + c) = to_half4(y);
+                }
             }
-        }
         lds_barrier();
         const int r0 = threadIdx.x / LPR, c8 = (threadIdx.x % LPR) * 8;
 #pragma unroll
