@@ -36,8 +36,8 @@ hipError_t launch_qkv_rope(const QkvArgs& a, hipStream_t s) {
 
 hipError_t launch_resid(const ResidArgs& a, hipStream_t s) {
     const int tiles = tiles_for<ResidTile>(a.rows, kHidden);
-    return a.stats ? launch<ResidTile>(gemm::resid_kernel<ResidTile, true>, tiles, a, s)
-                   : launch<ResidTile>(gemm::resid_kernel<ResidTile, false>, tiles, a, s);
+    return a.stats ? launch<ResidTile>(gemm::resid_kernel<ResidTile, true, 2>, tiles, a, s)
+                   : launch<ResidTile>(gemm::resid_kernel<ResidTile, false, 2>, tiles, a, s);
 }
 
 hipError_t launch_swiglu(const SwigluArgs& a, hipStream_t s) {

@@ -164,54 +164,62 @@ __device__ __forceinline__ int xcd_tile(int total) {
     return (g >> 3) < per && t < total ? t : -1;
 }
 
-// The pipelined K loop of one tile; k_tiles must be even (host-checked:
-// K % 128 == 0, so K / BK is even for BK 64 and 32). The loaders take the tile origin (m0, n0) and the stage.
-template <class T, class AL, class WL>
-__device__ __forceinline__ void gemm_main(AL (&al)[2], WL (&wl)[2], int m0, int n0, int k_tiles, half_t* lds,
+// The pipelined K loop of one tile with P register sets (P = 2 or 3) and two
+// LDS buffers: at step s the workgroup computes stage s from LDS buffer s%2,
+// the loads of stage s+P go into register set s%P (whose stage s is already
+// in LDS), and register set (s+1)%P, loaded P-1 steps earlier, is written to
+// buffer (s+1)%2 (which held stage s-1, finished by every wave at the
+// previous barrier). P = 3 gives each load two steps of latency cover for 32
+// more VGPRs. Loads past the last stage repeat it (unconditional loads keep
+// the compiler's vmcnt waits exact). The loaders take the tile origin
+// (m0, n0) and the stage.
+template <class T, int P, class AL, class WL>
+__device__ __forceinline__ void gemm_main(AL (&al)[P], WL (&wl)[P], int m0, int n0, int k_tiles, half_t* lds,
                                           Acc<T>& acc) {
+    static_assert(P == 2 || P == 3, "register sets");
+    constexpr int L = P == 2 ? 2 : 6;  // steps per unrolled block: s%2 and s%P are compile-time
     const int tid = threadIdx.x;
 #pragma unroll
     for (int i = 0; i < T::FN; ++i)
 #pragma unroll
         for (int j = 0; j < T::FM; ++j) acc.v[i][j] = float16_t{};
-    half_t* const s0 = lds;
-    half_t* const s1 = lds + T::STAGE_HALFS;
     const int last = k_tiles - 1;
-    al[0].load(m0, n0, 0, tid);
-    wl[0].load(m0, n0, 0, tid);
-    al[1].load(m0, n0, min(1, last), tid);
-    wl[1].load(m0, n0, min(1, last), tid);
-    al[0].store(s0, tid);
-    wl[0].store(s0 + T::BM * T::LDK, tid);
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+        al[i].load(m0, n0, min(i, last), tid);
+        wl[i].load(m0, n0, min(i, last), tid);
+    }
+    al[0].store(lds, tid);
+    wl[0].store(lds + T::BM * T::LDK, tid);
     lds_barrier();
-    for (int kt = 0; kt < k_tiles; kt += 2) {
-        // s0 holds stage kt; register set 1 holds stage kt+1 (maybe in flight).
-        al[0].load(m0, n0, min(kt + 2, last), tid);
-        wl[0].load(m0, n0, min(kt + 2, last), tid);
-        mma_stage<T>(s0, tid, acc);
-        al[1].store(s1, tid);
-        wl[1].store(s1 + T::BM * T::LDK, tid);
-        lds_barrier();
-        al[1].load(m0, n0, min(kt + 3, last), tid);
-        wl[1].load(m0, n0, min(kt + 3, last), tid);
-        mma_stage<T>(s1, tid, acc);
-        if (kt + 2 < k_tiles) {
-            al[0].store(s0, tid);
-            wl[0].store(s0 + T::BM * T::LDK, tid);
+    for (int base = 0; base < k_tiles; base += L) {
+#pragma unroll
+        for (int i = 0; i < L; ++i) {
+            const int s = base + i;
+            if (s >= k_tiles) break;  // uniform
+            half_t* const cur = lds + (i % 2) * T::STAGE_HALFS;
+            half_t* const nxt = lds + ((i + 1) % 2) * T::STAGE_HALFS;
+            al[i % P].load(m0, n0, min(s + P, last), tid);
+            wl[i % P].load(m0, n0, min(s + P, last), tid);
+            mma_stage<T>(cur, tid, acc);
+            if (s + 1 < k_tiles) {
+                al[(i + 1) % P].store(nxt, tid);
+                wl[(i + 1) % P].store(nxt + T::BM * T::LDK, tid);
+            }
+            lds_barrier();
         }
-        lds_barrier();
     }
 }
 
 // Runs the tile of this workgroup (if any) and its epilogue epi(acc, m0, n0).
-template <class T, class AL, class WL, class Epi>
-__device__ __forceinline__ void gemm_tile(AL (&al)[2], WL (&wl)[2], int n_tiles, int total_tiles, int k_tiles,
+template <class T, int P, class AL, class WL, class Epi>
+__device__ __forceinline__ void gemm_tile(AL (&al)[P], WL (&wl)[P], int n_tiles, int total_tiles, int k_tiles,
                                           half_t* lds, Epi&& epi) {
     const int t = xcd_tile(total_tiles);
     if (t < 0) return;  // uniform per workgroup
     const int n0 = (t % n_tiles) * T::BN, m0 = (t / n_tiles) * T::BM;
     Acc<T> acc;
-    gemm_main<T>(al, wl, m0, n0, k_tiles, lds, acc);
+    gemm_main<T, P>(al, wl, m0, n0, k_tiles, lds, acc);
     epi(acc, m0, n0);
 }
 

@@ -230,18 +230,25 @@ __global__ __launch_bounds__(T::THREADS) void qkv_rope_kernel(QkvArgs p) {
 }
 
 // Residual GEMM: x += ls * (A W^T + b), in place on the f16 residual stream
-// (with STATS, also the LayerNorm row statistics of the updated x). Each wave
+// (with STATS, also the LayerNorm row statistics of the updated x); P
+// register sets in the K loop (a third set measured no faster, even for the
+// K = 1536 down projection). Each wave
 // stages its f32 update (32 x 64) in LDS, then reads and writes x as
 // 128-byte row pieces, 8 lanes per row.
-template <class T, bool STATS>
+template <class T, bool STATS, int P>
 __global__ __launch_bounds__(T::THREADS) void resid_kernel(ResidArgs p) {
     static_assert(T::TN == 64, "one statistics slot per wave");
     constexpr int SPF = T::TN + 4;  // staging pitch in floats
     static_assert(T::WAVES * T::TM * SPF * 4 <= T::LDS_BYTES, "staging fits the stage buffers");
     __shared__ __attribute__((aligned(16))) half_t lds[T::LDS_HALFS];
     constexpr int NT = kHidden / T::BN;
-    ActRows<T> al[2] = {{{}, p.a, p.k, p.rows, 0}, {{}, p.a, p.k, p.rows, 0}};
-    WeightRows<T> wl[2] = {{{}, p.w, p.k, 0}, {{}, p.w, p.k, 0}};
+    ActRows<T> al[P];
+    WeightRows<T> wl[P];
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+        al[i] = ActRows<T>{{}, p.a, p.k, p.rows, 0};
+        wl[i] = WeightRows<T>{{}, p.w, p.k, 0};
+    }
     gemm_tile<T>(al, wl, NT, NT * ((p.rows + T::BM - 1) / T::BM), p.k / T::BK, lds,
                        [&](const Acc<T>& acc, int m0, int n0) {
         const Frag<T> f(m0, n0);
