@@ -11,6 +11,7 @@
 #include <map>
 #include <stdexcept>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../../include/dinov3_engine.h"
@@ -43,6 +44,14 @@ struct dhx_engine {
     std::map<uint64_t, Recorded> graphs;
     void* readback = nullptr;
     uint64_t readback_bytes = 0;
+    // Pipelined transfers: per slot a pinned input and output staging buffer
+    // and events marking the end of its upload, graph and readback.
+    hipStream_t up = nullptr, down = nullptr;
+    void* pin_in[DHX_STAGING_SLOTS] = {};
+    void* pin_out[DHX_STAGING_SLOTS] = {};
+    uint64_t pin_in_bytes = 0, pin_out_bytes = 0;
+    hipEvent_t in_done[DHX_STAGING_SLOTS] = {}, graph_done[DHX_STAGING_SLOTS] = {},
+               out_done[DHX_STAGING_SLOTS] = {};
     bool failed = false;
     bool fail_next = false;
     std::string error;
@@ -281,6 +290,51 @@ int guarded(dhx_engine* e, F&& f) {
     }
 }
 
+void release_staging(dhx_engine* e) {
+    for (hipStream_t* st : {&e->up, &e->down})
+        if (*st) {
+            (void)hipStreamSynchronize(*st);
+            (void)hipStreamDestroy(*st);
+            *st = nullptr;
+        }
+    for (int i = 0; i < DHX_STAGING_SLOTS; ++i) {
+        for (hipEvent_t* ev : {&e->in_done[i], &e->graph_done[i], &e->out_done[i]})
+            if (*ev) {
+                (void)hipEventDestroy(*ev);
+                *ev = nullptr;
+            }
+        if (e->pin_in[i]) (void)hipHostFree(e->pin_in[i]);
+        if (e->pin_out[i]) (void)hipHostFree(e->pin_out[i]);
+        e->pin_in[i] = e->pin_out[i] = nullptr;
+    }
+    e->pin_in_bytes = e->pin_out_bytes = 0;
+}
+
+// memcpy split over host threads: pageable <-> pinned copies of tens of MB
+// run at a few GB/s on one core, far below the PCIe link.
+void parallel_copy(void* dst, const void* src, uint64_t n) {
+    constexpr uint64_t kChunk = 4ull << 20;
+    const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
+    const unsigned threads = (unsigned)std::min<uint64_t>(std::min(16u, hw), (n + kChunk - 1) / kChunk);
+    if (threads <= 1) {
+        if (n) std::memcpy(dst, src, n);
+        return;
+    }
+    std::vector<std::thread> pool;
+    const uint64_t per = (n + threads - 1) / threads;
+    for (unsigned t = 0; t < threads; ++t) {
+        const uint64_t a = t * per, b = std::min(n, a + per);
+        if (a >= b) break;
+        pool.emplace_back([=] { std::memcpy(static_cast<char*>(dst) + a, static_cast<const char*>(src) + a, b - a); });
+    }
+    for (auto& th : pool) th.join();
+}
+
+void check_slot(const dhx_engine* e, uint32_t slot) {
+    if (slot >= DHX_STAGING_SLOTS) throw dhx::Error("staging slot must be 0 or 1");
+    if (!e->up) throw dhx::Error("staging was not reserved");
+}
+
 }  // namespace
 
 extern "C" {
@@ -318,6 +372,7 @@ void dhx_engine_free(dhx_engine* e) {
     if (!e) return;
     (void)hipSetDevice(e->device);
     if (e->stream) (void)hipStreamSynchronize(e->stream);
+    release_staging(e);  // waits for the transfer streams before their buffers go
     for (auto& kv : e->graphs)
         if (kv.second.exec) (void)hipGraphExecDestroy(kv.second.exec);
     for (void* b : e->buffers) (void)hipFree(b);
@@ -468,6 +523,88 @@ int dhx_read(dhx_engine* e, dhx_region r, void* out, uint64_t n) {
         hip_check(e, hipMemcpyAsync(e->readback, region_ptr(e, r), n, hipMemcpyDeviceToHost, e->stream), "readback copy");
         hip_check(e, hipStreamSynchronize(e->stream), "readback synchronize");
         std::memcpy(out, e->readback, n);
+    });
+}
+
+int dhx_reserve_staging(dhx_engine* e, uint64_t in_bytes, uint64_t out_bytes) {
+    return guarded(e, [&] {
+        ensure_usable(e);
+        set_device(e);
+        release_staging(e);
+        hip_check(e, hipStreamCreateWithFlags(&e->up, hipStreamNonBlocking), "hipStreamCreate");
+        hip_check(e, hipStreamCreateWithFlags(&e->down, hipStreamNonBlocking), "hipStreamCreate");
+        for (int i = 0; i < DHX_STAGING_SLOTS; ++i) {
+            hip_check(e, hipHostMalloc(&e->pin_in[i], std::max<uint64_t>(in_bytes, 16), hipHostMallocDefault),
+                      "hipHostMalloc");
+            hip_check(e, hipHostMalloc(&e->pin_out[i], std::max<uint64_t>(out_bytes, 16), hipHostMallocDefault),
+                      "hipHostMalloc");
+            for (hipEvent_t* ev : {&e->in_done[i], &e->graph_done[i], &e->out_done[i]})
+                hip_check(e, hipEventCreateWithFlags(ev, hipEventDisableTiming), "hipEventCreate");
+            // Completed events, so the first use of each slot waits for nothing.
+            hip_check(e, hipEventRecord(e->in_done[i], e->up), "hipEventRecord");
+            hip_check(e, hipEventRecord(e->graph_done[i], e->stream), "hipEventRecord");
+            hip_check(e, hipEventRecord(e->out_done[i], e->down), "hipEventRecord");
+        }
+        e->pin_in_bytes = in_bytes;
+        e->pin_out_bytes = out_bytes;
+    });
+}
+
+int dhx_copy_in(dhx_engine* e, dhx_region dst, const void* src, uint64_t n, uint32_t slot) {
+    return guarded(e, [&] {
+        ensure_usable(e);
+        check_slot(e, slot);
+        check_region(e, dst);
+        if (n > dst.bytes) throw dhx::Error("input exceeds allocated region");
+        if (n > e->pin_in_bytes) throw dhx::Error("input exceeds reserved staging");
+        if (n && !src) throw dhx::Error("null input");
+        set_device(e);
+        hip_check(e, hipEventSynchronize(e->in_done[slot]), "upload wait");  // staging buffer free again
+        parallel_copy(e->pin_in[slot], src, n);
+        hip_check(e, hipStreamWaitEvent(e->up, e->graph_done[slot], 0), "hipStreamWaitEvent");
+        hip_check(e, hipMemcpyAsync(region_ptr(e, dst), e->pin_in[slot], n, hipMemcpyHostToDevice, e->up), "upload");
+        hip_check(e, hipEventRecord(e->in_done[slot], e->up), "hipEventRecord");
+    });
+}
+
+int dhx_replay_slot(dhx_engine* e, uint64_t batch, uint32_t slot) {
+    return guarded(e, [&] {
+        ensure_usable(e);
+        check_slot(e, slot);
+        auto it = e->graphs.find(batch);
+        if (it == e->graphs.end()) throw dhx::Error("batch has not been prepared");
+        set_device(e);
+        hip_check(e, hipStreamWaitEvent(e->stream, e->in_done[slot], 0), "hipStreamWaitEvent");
+        hip_check(e, hipStreamWaitEvent(e->stream, e->out_done[slot], 0), "hipStreamWaitEvent");
+        hip_check(e, hipGraphLaunch(it->second.exec, e->stream), "graph launch");
+        hip_check(e, hipEventRecord(e->graph_done[slot], e->stream), "hipEventRecord");
+    });
+}
+
+int dhx_copy_out(dhx_engine* e, dhx_region src, uint64_t n, uint32_t slot) {
+    return guarded(e, [&] {
+        ensure_usable(e);
+        check_slot(e, slot);
+        check_region(e, src);
+        if (n > src.bytes) throw dhx::Error("output exceeds allocated region");
+        if (n > e->pin_out_bytes) throw dhx::Error("output exceeds reserved staging");
+        set_device(e);
+        hip_check(e, hipStreamWaitEvent(e->down, e->graph_done[slot], 0), "hipStreamWaitEvent");
+        hip_check(e, hipMemcpyAsync(e->pin_out[slot], region_ptr(e, src), n, hipMemcpyDeviceToHost, e->down),
+                  "readback copy");
+        hip_check(e, hipEventRecord(e->out_done[slot], e->down), "hipEventRecord");
+    });
+}
+
+int dhx_copy_out_finish(dhx_engine* e, void* dst, uint64_t n, uint32_t slot) {
+    return guarded(e, [&] {
+        ensure_usable(e);
+        check_slot(e, slot);
+        if (n > e->pin_out_bytes) throw dhx::Error("output exceeds reserved staging");
+        if (n && !dst) throw dhx::Error("null output");
+        set_device(e);
+        hip_check(e, hipEventSynchronize(e->out_done[slot]), "readback wait");
+        parallel_copy(dst, e->pin_out[slot], n);
     });
 }
 

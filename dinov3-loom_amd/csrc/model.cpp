@@ -9,6 +9,7 @@
 #include <memory>
 #include <string>
 #include <sys/stat.h>
+#include <thread>
 #include <vector>
 
 #include "../../include/dinov3.h"
@@ -71,6 +72,29 @@ void check(int rc, dhx_engine* e) {
     if (rc != 0) throw Error(dhx_last_error(e));
 }
 
+// Finite check of the whole input before any GPU work (lib.rs validates
+// every pixel first), split over host threads for large batches.
+bool all_finite(const float* p, uint64_t n) {
+    auto scan = [p](uint64_t a, uint64_t b) {
+        bool ok = true;
+        for (uint64_t i = a; i < b; ++i) ok &= std::isfinite(p[i]);
+        return ok;
+    };
+    constexpr uint64_t kChunk = 1ull << 20;
+    const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
+    const unsigned threads = (unsigned)std::min<uint64_t>(std::min(16u, hw), (n + kChunk - 1) / kChunk);
+    if (threads <= 1) return scan(0, n);
+    std::vector<std::thread> pool;
+    std::vector<char> ok(threads, 1);
+    const uint64_t per = (n + threads - 1) / threads;
+    for (unsigned t = 0; t < threads; ++t)
+        pool.emplace_back([&, t] { ok[t] = scan(t * per, std::min(n, (t + 1) * per)); });
+    for (auto& th : pool) th.join();
+    for (char v : ok)
+        if (!v) return false;
+    return true;
+}
+
 }  // namespace
 
 class Model {
@@ -97,12 +121,15 @@ public:
         const uint64_t heads = B * 6 * tpad_ * 64 * 2;
         // x, h, attn and act are f16; q/k/v are f16 head-major (padded rows
         // stay zero); out, the NCHW images, the split-K slabs and the
-        // LayerNorm row statistics of x are f32.
+        // LayerNorm row statistics of x are f32. The images and out exist
+        // twice (one per transfer slot) so that consecutive chunks of a
+        // forward overlap their uploads and readbacks with each other's graph.
         const uint64_t sizes[kBuffers] = {r * kHiddenU * 2, r * kHiddenU * 2, heads, heads, heads, r * kHiddenU * 2,
                                           r * 1536 * 2,     r * kHiddenU * 4, B * image_elems_ * 4,
-                                          (uint64_t)kSplits * r * kHiddenU * 4, r * 12 * 4};
+                                          (uint64_t)kSplits * r * kHiddenU * 4, r * 12 * 4,
+                                          r * kHiddenU * 4, B * image_elems_ * 4};
         for (int i = 0; i < kBuffers; ++i) check(dhx_allocate(e, sizes[i], &a_[i]), e);
-        check(dhx_reserve_readback(e, B * tokens_ * kHiddenU * 4), e);
+        check(dhx_reserve_staging(e, B * image_elems_ * 4, r * kHiddenU * 4), e);
     }
 
     dhx_engine* engine() { return engine_.get(); }
@@ -124,16 +151,36 @@ public:
         branches_ = n;
     }
 
-    // lib.rs:90-114
+    // lib.rs:90-114: chunks of max_batch images, pipelined over the two
+    // transfer slots: chunk i uses slot i % 2, so its host copy and upload
+    // run while chunk i-1's graph runs, and chunk i-1's readback and host
+    // copy while chunk i's graph runs. Results are those of the chunks run
+    // one at a time.
     void forward(const float* pixels, uint64_t n, float* out, uint64_t out_floats) {
         check_input(pixels, n);
         const uint64_t batch = n / image_elems_;
         const uint64_t per_image = tokens_ * kHiddenU;
         if (out_floats < batch * per_image) throw Error("output buffer holds fewer than images*tokens*384 floats");
-        for (uint64_t first = 0; first < batch; first += opts_.max_batch) {
-            const uint64_t b = std::min<uint64_t>(opts_.max_batch, batch - first);
-            stage(pixels + first * image_elems_, b);
-            check(dhx_read(engine_.get(), region(kOut), out + first * per_image, b * per_image * 4), engine_.get());
+        if (batch == 0) return;
+        dhx_engine* e = engine_.get();
+        const uint64_t chunks = (batch + opts_.max_batch - 1) / opts_.max_batch;
+        auto size_of = [&](uint64_t i) { return std::min<uint64_t>(opts_.max_batch, batch - i * opts_.max_batch); };
+        for (uint64_t i = 0; i < std::min<uint64_t>(chunks, 2); ++i) prepare(size_of(i), (uint32_t)(i & 1));
+        if (chunks > 2) prepare(size_of(chunks - 1), (uint32_t)((chunks - 1) & 1));  // the tail chunk
+        for (uint64_t i = 0; i <= chunks; ++i) {
+            if (i < chunks) {
+                const uint32_t slot = (uint32_t)(i & 1);
+                const uint64_t b = size_of(i), first = i * opts_.max_batch;
+                check(dhx_copy_in(e, a_[image_buffer(slot)], pixels + first * image_elems_, b * image_elems_ * 4, slot), e);
+                check(dhx_replay_slot(e, key(b, slot), slot), e);
+                check(dhx_copy_out(e, a_[out_buffer(slot)], b * per_image * 4, slot), e);
+            }
+            if (i > 0) {
+                const uint64_t j = i - 1;
+                check(dhx_copy_out_finish(e, out + j * opts_.max_batch * per_image, size_of(j) * per_image * 4,
+                                          (uint32_t)(j & 1)),
+                      e);
+            }
         }
     }
 
@@ -149,8 +196,7 @@ public:
     void check_input(const float* pixels, uint64_t n) const {
         if (n % image_elems_ != 0)
             throw Error("input must contain complete 3×" + std::to_string(size_) + "×" + std::to_string(size_) + " images");
-        for (uint64_t i = 0; i < n; ++i)
-            if (!std::isfinite(pixels[i])) throw Error("input must be finite");
+        if (!all_finite(pixels, n)) throw Error("input must be finite");
     }
 
     // lib.rs:116-124
@@ -173,22 +219,22 @@ public:
     // into the QKV and gate/up GEMMs, fed by row statistics that the
     // producers of x write (62 launches per group at b > 1); the unfused plan
     // runs LayerNorm kernels as the reference does (86).
-    void prepare(uint64_t b) {
-        if (dhx_has_graph(engine_.get(), key(b))) return;
+    void prepare(uint64_t b, uint32_t slot = 0) {
+        if (dhx_has_graph(engine_.get(), key(b, slot))) return;
         const uint32_t nb = groups(b);
         std::vector<dhx_launch> l;
         std::vector<uint64_t> counts;
         for (uint32_t g = 0; g < nb; ++g) {
             const uint64_t first = b * g / nb, end = b * (g + 1) / nb;
             const size_t before = l.size();
-            plan(first, end - first, b, l);
+            plan(first, end - first, b, slot, l);
             counts.push_back(l.size() - before);
         }
-        check(dhx_record_branches(engine_.get(), key(b), l.data(), counts.data(), nb), engine_.get());
+        check(dhx_record_branches(engine_.get(), key(b, slot), l.data(), counts.data(), nb), engine_.get());
     }
 
     // The launches for images [first, first + n) of a batch of b.
-    void plan(uint64_t first, uint64_t n, uint64_t b, std::vector<dhx_launch>& l) const {
+    void plan(uint64_t first, uint64_t n, uint64_t b, uint32_t slot, std::vector<dhx_launch>& l) const {
         const uint32_t r = (uint32_t)(n * tokens_);
         const uint32_t B = (uint32_t)n, G = grid_, TP = (uint32_t)tpad_;
         auto add = [&](uint32_t kernel, std::initializer_list<uint32_t> s, std::initializer_list<dhx_region> bind) {
@@ -213,7 +259,7 @@ public:
         const dhx_region X = part(kX, row * 2), H = part(kH, row * 2), S = part(kStats, tokens_ * 12 * 4);
         const dhx_region Q = part(kQ, heads), K = part(kK, heads), V = part(kV, heads);
         const dhx_region A = part(kAttn, row * 2), F = part(kAct, tokens_ * 1536 * 2);
-        const dhx_region O = part(kOut, row * 4), I = part(kImage, image_elems_ * 4);
+        const dhx_region O = part(out_buffer(slot), row * 4), I = part(image_buffer(slot), image_elems_ * 4);
         const dhx_region SL = part(kPartials, (uint64_t)kSplits * row * 4);  // [splits][rows][384] per group
         const bool split = b == 1 || splitk_ == 1;
         if (fused_ln_) {
@@ -268,13 +314,15 @@ public:
     }
 
     // Graph key: batch size plus one bit per plan variant.
-    uint64_t key(uint64_t b) const {
+    uint64_t key(uint64_t b, uint32_t slot = 0) const {
         return b | (splitk_ && b > 1 ? (1ull << 32) : 0) | (fused_ln_ ? 0 : (1ull << 33)) |
-               ((uint64_t)(groups(b) - 1) << 34);
+               ((uint64_t)(groups(b) - 1) << 34) | ((uint64_t)slot << 36);
     }
 
 private:
-    enum { kX, kH, kQ, kK, kV, kAttn, kAct, kOut, kImage, kPartials, kStats, kBuffers };
+    enum { kX, kH, kQ, kK, kV, kAttn, kAct, kOut, kImage, kPartials, kStats, kOut1, kImage1, kBuffers };
+    static int image_buffer(uint32_t slot) { return slot ? kImage1 : kImage; }
+    static int out_buffer(uint32_t slot) { return slot ? kOut1 : kOut; }
     struct EngineFree {
         void operator()(dhx_engine* e) const { dhx_engine_free(e); }
     };

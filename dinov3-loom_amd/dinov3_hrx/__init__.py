@@ -119,6 +119,11 @@ def _load_library() -> ctypes.CDLL:
     L.dhx_dispatch.argtypes = [vp, c.c_uint64]
     L.dhx_reserve_readback.argtypes = [vp, c.c_uint64]
     L.dhx_read.argtypes = [vp, Region, vp, c.c_uint64]
+    L.dhx_reserve_staging.argtypes = [vp, c.c_uint64, c.c_uint64]
+    L.dhx_copy_in.argtypes = [vp, Region, vp, c.c_uint64, c.c_uint32]
+    L.dhx_replay_slot.argtypes = [vp, c.c_uint64, c.c_uint32]
+    L.dhx_copy_out.argtypes = [vp, Region, c.c_uint64, c.c_uint32]
+    L.dhx_copy_out_finish.argtypes = [vp, vp, c.c_uint64, c.c_uint32]
     L.dhx_benchmark.argtypes = [vp, c.c_uint64, c.c_uint64, c.POINTER(_Timings)]
     return L
 
@@ -392,6 +397,25 @@ class Engine:
 
     def synchronize(self) -> None:
         self._c(_lib.dhx_synchronize(self._h))
+
+    def reserve_staging(self, in_bytes: int, out_bytes: int) -> None:
+        """Pinned staging for the pipelined transfers (two slots)."""
+        self._c(_lib.dhx_reserve_staging(self._h, int(in_bytes), int(out_bytes)))
+
+    def copy_in(self, region: Region, array: np.ndarray, slot: int) -> None:
+        a = np.ascontiguousarray(array)
+        self._c(_lib.dhx_copy_in(self._h, region, a.ctypes.data, a.nbytes, int(slot)))
+
+    def replay_slot(self, key: int, slot: int) -> None:
+        self._c(_lib.dhx_replay_slot(self._h, int(key), int(slot)))
+
+    def copy_out(self, region: Region, nbytes: int, slot: int) -> None:
+        self._c(_lib.dhx_copy_out(self._h, region, int(nbytes), int(slot)))
+
+    def copy_out_finish(self, dtype, shape, slot: int) -> np.ndarray:
+        out = np.empty(shape, dtype)
+        self._c(_lib.dhx_copy_out_finish(self._h, out.ctypes.data, out.nbytes, int(slot)))
+        return out
 
     def reserve_readback(self, nbytes: int) -> None:
         self._c(_lib.dhx_reserve_readback(self._h, int(nbytes)))

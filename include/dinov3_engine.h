@@ -149,6 +149,31 @@ int dhx_read(dhx_engine *e, dhx_region r, void *out, uint64_t n);
  * graph replay and direct dispatch in alternating order, first 10 dropped. */
 int dhx_benchmark(dhx_engine *e, uint64_t batch, uint64_t samples, dhx_timings *out);
 
+/* Pipelined transfers (no reference counterpart; the reference uploads,
+ * replays and reads back one chunk at a time, lib.rs:98-112). Two slots,
+ * each with a pinned input and a pinned output staging buffer, a stream for
+ * uploads and one for readbacks, so chunk i+1's host copy and upload overlap
+ * chunk i's graph, and chunk i's readback overlaps chunk i+1's graph. Host
+ * copies into and out of staging run on several threads. Slot s's graphs
+ * must read their input from the region dhx_copy_in filled for slot s and
+ * write their output to the region dhx_copy_out reads for slot s.
+ *   dhx_reserve_staging: allocate the staging buffers (in_bytes / out_bytes
+ *     per slot) and the streams and events.
+ *   dhx_copy_in: wait until slot s's previous upload has left its staging
+ *     buffer, copy n bytes from host into it, then upload them to dst once
+ *     slot s's previous graph is done with dst.
+ *   dhx_replay_slot: launch `batch`'s graph after slot s's upload and after
+ *     slot s's previous readback (which reads the graph's output region).
+ *   dhx_copy_out: read back n bytes of src into slot s's staging buffer once
+ *     slot s's graph is done.
+ *   dhx_copy_out_finish: wait for that readback and copy it to host memory. */
+#define DHX_STAGING_SLOTS 2
+int dhx_reserve_staging(dhx_engine *e, uint64_t in_bytes, uint64_t out_bytes);
+int dhx_copy_in(dhx_engine *e, dhx_region dst, const void *src, uint64_t n, uint32_t slot);
+int dhx_replay_slot(dhx_engine *e, uint64_t batch, uint32_t slot);
+int dhx_copy_out(dhx_engine *e, dhx_region src, uint64_t n, uint32_t slot);
+int dhx_copy_out_finish(dhx_engine *e, void *dst, uint64_t n, uint32_t slot);
+
 /* No reference counterpart (measurement hook): average device time of each
  * launch of `batch`'s list, from HIP events on the engine's stream over
  * `iters` direct dispatches of that launch alone. ms_out has one slot per

@@ -65,6 +65,42 @@ def check(gpu, ref, atol, rel=2.0**-10, cos_min=0.99999, what=""):
     return err.max()
 
 
+def test_pipelined_transfer_slots(eng):
+    # Two slots, each: host -> pinned -> device upload, a graph over the
+    # uploaded rows, readback of its output -> pinned -> host. Six rounds
+    # alternate the slots with several rounds in flight at once; every result
+    # equals the LayerNorm of its own input.
+    with pytest.raises(d.DINOv3Error, match="staging was not reserved"):
+        eng.copy_out(eng.allocate(16), 16, 0)
+    rows = 2000
+    eng.reserve_staging(rows * 384 * 2, rows * 384 * 4)
+    g = np.ones(384, np.float32)
+    b = np.zeros(384, np.float32)
+    G, B = up(eng, g), up(eng, b)
+    xin = [eng.allocate(rows * 384 * 2) for _ in range(2)]
+    yout = [eng.allocate(rows * 384 * 4) for _ in range(2)]
+    keys = [next(_keys), next(_keys)]
+    for s in range(2):
+        eng.record(keys[s], [(K_LN32, [rows], [xin[s], G, B, yout[s]])])
+    rng = np.random.default_rng(9)
+    xs = [f16(rng.normal(size=(rows, 384)) * (1 + i)) for i in range(6)]
+    got = [None] * 6
+    for i in range(7):
+        if i < 6:
+            s = i % 2
+            eng.copy_in(xin[s], xs[i], s)
+            eng.replay_slot(keys[s], s)
+            eng.copy_out(yout[s], rows * 384 * 4, s)
+        if i > 0:
+            got[i - 1] = eng.copy_out_finish(np.float32, (rows, 384), (i - 1) % 2)
+    for i in range(6):
+        check(got[i], oracle.layernorm(xs[i].astype(np.float64), g, b), atol=2e-5, rel=1e-5, what=f"slot round {i}")
+    with pytest.raises(d.DINOv3Error, match="staging slot must be 0 or 1"):
+        eng.copy_in(xin[0], xs[0], 2)
+    with pytest.raises(d.DINOv3Error, match="exceeds reserved staging"):
+        eng.copy_out(eng.allocate(rows * 384 * 8), rows * 384 * 8, 0)
+
+
 def test_allocation_fill_is_ordered_before_upload(eng):
     # dhx_allocate zeroes a new region; the fill must complete before an
     # upload queued right after it (on the engine's own stream), or the

@@ -88,6 +88,19 @@ def test_chunking_and_empty(models):
     assert m.forward(np.zeros(0, np.float32)).shape == (0, 201, 384)
 
 
+def test_pipelined_chunks_equal_single_chunks(models):
+    # 9 chunks of 4 (the last of 2) alternate the two transfer slots with
+    # uploads, graphs and readbacks of neighbouring chunks overlapping; each
+    # chunk's rows equal the same images run alone.
+    m = models(1, max_batch=4)
+    px = d.random_pixels(12, 34)
+    out = m.forward(px)
+    assert out.shape == (34, 201, 384)
+    for first in (0, 4, 16, 28, 32):
+        n = min(4, 34 - first)
+        assert np.array_equal(out[first:first + n], m.forward(px[first:first + n])), first
+
+
 def test_cls_and_patch_mean(models):
     m = models(1)
     px = d.random_pixels(4, 3)
