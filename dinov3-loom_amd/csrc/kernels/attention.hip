@@ -35,7 +35,7 @@ __device__ __forceinline__ half8_t zero8() {
     return z;
 }
 
-__global__ __launch_bounds__(kThreads) void attention_kernel(AttentionArgs p) {
+__global__ __launch_bounds__(kThreads, 3) void attention_kernel(AttentionArgs p) {
     __shared__ half_t sK[2][KB * KLD];
     __shared__ half_t sV[2][KB * KLD];
     // 1-D grid, XCD-aware: the tile space (query block fastest, then head,
@@ -53,28 +53,33 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttentionArgs p) {
     const half_t* kg = p.k + bh * p.tpad * kHeadDim;
     const half_t* vg = p.v + bh * p.tpad * kHeadDim;
 
+    const int nkb = (T + KB - 1) / KB;
     const int qrow = qb * QB + wave * 32 + l32;
     half8_t qf[4];
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
         qf[kk] = qrow < T ? *(const half8_t*)(qg + (size_t)qrow * kHeadDim + kk * 16 + hi * 8) : zero8();
 
-    // Each thread moves two 16-byte pieces of the K block and two of V.
-    half8_t kr[2], vr[2];
-    auto load = [&](int kb) {
+    // Each thread moves two 16-byte pieces of the K block and two of V. Two
+    // register sets: the loads of block kb+2 are issued while block kb is
+    // computed, so each has two blocks of compute to land (a block is short
+    // next to an L2 round trip). Loads past the last block repeat it.
+    half8_t kr[2][2], vr[2][2];
+    auto load = [&](int set, int kb) {
+        kb = min(kb, nkb - 1);
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int c = tid + i * kThreads, row = c >> 3, col = (c & 7) * 8;
-            kr[i] = *(const half8_t*)(kg + (size_t)(kb * KB + row) * kHeadDim + col);
-            vr[i] = *(const half8_t*)(vg + (size_t)(kb * KB + row) * kHeadDim + col);
+            kr[set][i] = *(const half8_t*)(kg + (size_t)(kb * KB + row) * kHeadDim + col);
+            vr[set][i] = *(const half8_t*)(vg + (size_t)(kb * KB + row) * kHeadDim + col);
         }
     };
-    auto store = [&](int buf) {
+    auto store = [&](int set, int buf) {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int c = tid + i * kThreads, row = c >> 3, col = (c & 7) * 8;
-            *(half8_t*)(&sK[buf][row * KLD + col]) = kr[i];
-            *(half8_t*)(&sV[buf][row * KLD + col]) = vr[i];
+            *(half8_t*)(&sK[buf][row * KLD + col]) = kr[set][i];
+            *(half8_t*)(&sV[buf][row * KLD + col]) = vr[set][i];
         }
     };
 
@@ -91,33 +96,30 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttentionArgs p) {
     const float neg_inf = -__builtin_inff();
     float16_t o[2] = {float16_t{}, float16_t{}};
     float m_run = -1e30f, l_run = 0.f;
-    const int nkb = (T + KB - 1) / KB;
     // Waves whose 32 queries all lie past T only help move K and V.
     const bool active = qb * QB + wave * 32 < T;
 
-    load(0);
-    store(0);
-    __syncthreads();
-    for (int kb = 0; kb < nkb; ++kb) {
-        const int buf = kb & 1;
-        const bool more = kb + 1 < nkb;
-        if (more) load(kb + 1);
+    load(0, 0);
+    load(1, 1);
+    store(0, 0);
+    lds_barrier();
+    auto block = [&](int kb, int buf) {
 #pragma unroll
         for (int sub = 0; sub < 2 && active; ++sub) {
             const int key0 = kb * KB + sub * 32;
             if (key0 >= T) break;  // uniform across the workgroup
             float16_t s = {};
             const half_t* krow = &sK[buf][(sub * 32 + l32) * KLD + hi * 8];
-#pragma unroll
+    #pragma unroll
             for (int kk = 0; kk < 4; ++kk) s = mfma32x32x16(*(const half8_t*)(krow + kk * 16), qf[kk], s);
             // s[r] is the score of key key0 + 8(r/4) + 4*hi + r%4 for query l32.
             if (key0 + 32 > T) {  // the last, partial block of keys (uniform)
-#pragma unroll
+    #pragma unroll
                 for (int r = 0; r < 16; ++r)
                     if (key0 + 8 * (r >> 2) + 4 * hi + (r & 3) >= T) s[r] = neg_inf;
             }
             float mx = s[0];
-#pragma unroll
+    #pragma unroll
             for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
             mx = fmaxf(mx, __shfl_xor(mx, 32, 64));  // every sub-block holds a valid key of each pair
             // Lazy rescaling: the running max moves only when a score exceeds
@@ -134,7 +136,7 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttentionArgs p) {
             }
             const float mb = m_run * kLog2e;
             float sum = 0.f;
-#pragma unroll
+    #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 s[r] = fast_exp2(fmaf(s[r], kLog2e, -mb));
                 sum += s[r];
@@ -145,13 +147,13 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttentionArgs p) {
             // key0 + 16ks + (j < 4 ? 4hi + j : 8 + 4hi + j - 4); the V^T
             // transpose reads below give channel ct*32 + l32 of the same keys.
             half8_t pb[2];
-#pragma unroll
+    #pragma unroll
             for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
+    #pragma unroll
                 for (int e = 0; e < 8; ++e) pb[ks][e] = (half_t)s[8 * ks + e];
-#pragma unroll
+    #pragma unroll
             for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
+    #pragma unroll
                 for (int ks = 0; ks < 2; ++ks) {
                     const half_t* vb = &sV[buf][(sub * 32 + ks * 16 + 4 * hi + tr_row) * KLD + ct * 32 + tr_col];
                     const half4_t a0 = lds_read_tr16(vb), a1 = lds_read_tr16(vb + 8 * KLD);
@@ -159,8 +161,17 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttentionArgs p) {
                     o[ct] = mfma32x32x16(va, pb[ks], o[ct]);
                 }
         }
-        if (more) store(buf ^ 1);
-        __syncthreads();
+    };
+    for (int kb = 0; kb < nkb; kb += 2) {
+        load(0, kb + 2);
+        block(kb, 0);
+        if (kb + 1 < nkb) store(1, 1);
+        lds_barrier();
+        if (kb + 1 >= nkb) break;
+        load(1, kb + 3);
+        block(kb + 1, 1);
+        if (kb + 2 < nkb) store(0, 0);
+        lds_barrier();
     }
 
     if (qrow < T) {

@@ -43,6 +43,12 @@ __device__ __forceinline__ half4_t lds_read_tr16(const half_t* p) {
     return __builtin_bit_cast(half4_t, v);
 }
 
+// Waits for this wave's LDS reads and writes, then joins the workgroup
+// barrier; global loads stay in flight (__syncthreads() would also drain
+// them: its workgroup release fence waits on vmcnt(0)). The memory clobber
+// keeps the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // Orders this wave's earlier LDS writes before its later LDS reads (of words
 // other lanes wrote): a wave's LDS instructions complete in issue order, and
 // the clobber keeps the compiler from moving LDS accesses across this point.

@@ -42,11 +42,6 @@ struct Tile {
     static constexpr int LDS_BYTES = LDS_HALFS * 2;
 };
 
-// Waits for this wave's LDS reads and writes, then joins the workgroup
-// barrier; global loads stay in flight. The memory clobber keeps the
-// compiler from moving LDS accesses across it.
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
 __device__ __forceinline__ half8_t zero8() {
     half8_t z = {};
     return z;
