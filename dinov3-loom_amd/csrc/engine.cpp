@@ -95,6 +95,9 @@ struct Need {
 
 uint64_t tokens_for(uint32_t grid) { return (uint64_t)grid * grid + dhx::kPrefix; }
 
+// Bytes of an f16 activation matrix in fragment order (rows padded to 32).
+uint64_t frag(uint64_t rows, uint64_t k) { return (rows + 31) / 32 * 32 * k * 2; }
+
 // The shapes each kernel reads and writes, from its scalars; recording and
 // dispatch refuse any binding smaller than this (so no kernel can run past a
 // buffer) and any misaligned binding (kernels use 16-byte vector accesses).
@@ -111,15 +114,15 @@ Need required(const dhx_launch& l) {
             positive(s[0], "images");
             positive(s[1], "grid");
             const uint64_t side = 16ull * s[1], T = tokens_for(s[1]);
-            const uint64_t px = s[0] * 3 * side * side * 4, x = s[0] * T * H * 2;
+            const uint64_t px = s[0] * 3 * side * side * 4, x = frag(s[0] * T, H);
             if (l.kernel == DHX_K_PATCH_EMBED) return {5, {px, H * 768 * 2, H * 4, 5 * H * 4, x}};
             return {7, {px, H * 768 * 2, H * 4, 5 * H * 4, 5 * S, x, s[0] * T * S}};
         }
         case DHX_K_LAYERNORM:
         case DHX_K_LAYERNORM_F32: {
             positive(s[0], "rows");
-            const uint64_t out = l.kernel == DHX_K_LAYERNORM ? 2 : 4;
-            return {4, {s[0] * H * 2, H * 4, H * 4, s[0] * H * out}};
+            const uint64_t out = l.kernel == DHX_K_LAYERNORM ? frag(s[0], H) : s[0] * H * 4;
+            return {4, {frag(s[0], H), H * 4, H * 4, out}};
         }
         case DHX_K_QKV_ROPE:
         case DHX_K_QKV_ROPE_LN:
@@ -129,38 +132,38 @@ Need required(const dhx_launch& l) {
             const uint64_t T = tokens_for(s[1]), P = (uint64_t)s[1] * s[1];
             if (s[2] % 128 != 0 || s[2] < T) throw dhx::Error("tpad must be a multiple of 128 covering every token");
             const uint64_t heads = s[0] * dhx::kHeads * (uint64_t)s[2] * dhx::kHeadDim * 2;
-            if (l.kernel == DHX_K_ATTENTION) return {4, {heads, heads, heads, s[0] * T * H * 2}};
+            if (l.kernel == DHX_K_ATTENTION) return {4, {heads, heads, heads, frag(s[0] * T, H)}};
             if (l.kernel == DHX_K_QKV_ROPE)
-                return {8, {s[0] * T * H * 2, 3 * H * H * 2, 3 * H * 4, P * 64 * 4, P * 64 * 4, heads, heads, heads}};
-            return {10, {s[0] * T * H * 2, s[0] * T * S, 3 * H * H * 2, 3 * H * 4, 3 * H * 4, P * 64 * 4, P * 64 * 4,
+                return {8, {frag(s[0] * T, H), 3 * H * H * 2, 3 * H * 4, P * 64 * 4, P * 64 * 4, heads, heads, heads}};
+            return {10, {frag(s[0] * T, H), s[0] * T * S, 3 * H * H * 2, 3 * H * 4, 3 * H * 4, P * 64 * 4, P * 64 * 4,
                          heads, heads, heads}};
         }
         case DHX_K_RESID:
         case DHX_K_RESID_STATS: {
             positive(s[0], "rows");
             if (s[1] == 0 || s[1] % 128 != 0) throw dhx::Error("k must be a positive multiple of 128");
-            std::vector<uint64_t> b = {s[0] * (uint64_t)s[1] * 2, H * s[1] * 2, H * 4, H * 4, s[0] * H * 2};
+            std::vector<uint64_t> b = {frag(s[0], s[1]), H * s[1] * 2, H * 4, H * 4, frag(s[0], H)};
             if (l.kernel == DHX_K_RESID_STATS) b.push_back(s[0] * S);
             return {(uint32_t)b.size(), b};
         }
         case DHX_K_SWIGLU:
             positive(s[0], "rows");
-            return {4, {s[0] * H * 2, 2ull * dhx::kFF * H * 2, 2ull * dhx::kFF * 4, s[0] * (uint64_t)dhx::kFF * 2}};
+            return {4, {frag(s[0], H), 2ull * dhx::kFF * H * 2, 2ull * dhx::kFF * 4, frag(s[0], dhx::kFF)}};
         case DHX_K_SWIGLU_LN:
             positive(s[0], "rows");
-            return {6, {s[0] * H * 2, s[0] * S, 2ull * dhx::kFF * H * 2, 2ull * dhx::kFF * 4, 2ull * dhx::kFF * 4,
-                        s[0] * (uint64_t)dhx::kFF * 2}};
+            return {6, {frag(s[0], H), s[0] * S, 2ull * dhx::kFF * H * 2, 2ull * dhx::kFF * 4, 2ull * dhx::kFF * 4,
+                        frag(s[0], dhx::kFF)}};
         case DHX_K_SPLITK: {
             positive(s[0], "rows");
             positive(s[2], "splits");
             if (s[1] == 0 || s[1] % (128ull * s[2]) != 0) throw dhx::Error("k must split into multiples of 128");
-            return {3, {s[0] * (uint64_t)s[1] * 2, H * s[1] * 2, (uint64_t)s[2] * s[0] * H * 4}};
+            return {3, {frag(s[0], s[1]), H * s[1] * 2, (uint64_t)s[2] * s[0] * H * 4}};
         }
         case DHX_K_SPLITK_REDUCE:
         case DHX_K_SPLITK_REDUCE_STATS: {
             positive(s[0], "rows");
             positive(s[1], "splits");
-            std::vector<uint64_t> b = {(uint64_t)s[1] * s[0] * H * 4, H * 4, H * 4, s[0] * H * 2};
+            std::vector<uint64_t> b = {(uint64_t)s[1] * s[0] * H * 4, H * 4, H * 4, frag(s[0], H)};
             if (l.kernel == DHX_K_SPLITK_REDUCE_STATS) b.push_back(s[0] * S);
             return {(uint32_t)b.size(), b};
         }
@@ -524,6 +527,38 @@ int dhx_read(dhx_engine* e, dhx_region r, void* out, uint64_t n) {
         hip_check(e, hipStreamSynchronize(e->stream), "readback synchronize");
         std::memcpy(out, e->readback, n);
     });
+}
+
+int dhx_fragment_order(const uint16_t* rows_in, uint64_t rows, uint64_t k, uint16_t* frag_out) {
+    try {
+        if (k % 16 != 0 || (rows && (!rows_in || !frag_out))) throw dhx::Error("fragment order needs k % 16 == 0");
+        const uint64_t padded = (rows + 31) / 32 * 32;
+        std::memset(frag_out, 0, padded * k * 2);
+        for (uint64_t m = 0; m < rows; ++m)
+            for (uint64_t c = 0; c < k; c += 8) {
+                const uint64_t o = ((m / 32) * (k / 16) + c / 16) * 512 + ((c / 8) % 2 * 32 + m % 32) * 8;
+                std::memcpy(frag_out + o, rows_in + m * k + c, 16);
+            }
+        return 0;
+    } catch (const std::exception& ex) {
+        dhx::set_global_error(ex.what());
+        return 1;
+    }
+}
+
+int dhx_row_order(const uint16_t* frag_in, uint64_t rows, uint64_t k, uint16_t* rows_out) {
+    try {
+        if (k % 16 != 0 || (rows && (!frag_in || !rows_out))) throw dhx::Error("fragment order needs k % 16 == 0");
+        for (uint64_t m = 0; m < rows; ++m)
+            for (uint64_t c = 0; c < k; c += 8) {
+                const uint64_t o = ((m / 32) * (k / 16) + c / 16) * 512 + ((c / 8) % 2 * 32 + m % 32) * 8;
+                std::memcpy(rows_out + m * k + c, frag_in + o, 16);
+            }
+        return 0;
+    } catch (const std::exception& ex) {
+        dhx::set_global_error(ex.what());
+        return 1;
+    }
 }
 
 int dhx_reserve_staging(dhx_engine* e, uint64_t in_bytes, uint64_t out_bytes) {

@@ -175,16 +175,19 @@ __global__ __launch_bounds__(kThreads, 3) void attention_kernel(AttentionArgs p)
     }
 
     if (qrow < T) {
+        // out is in fragment order: the lane's 4 channels are half of one
+        // 8-channel piece of row img*T + qrow (the partner lane l ^ 32 holds
+        // the other half), so the 32 queries of a wave fill whole pieces.
         const float inv = 1.0f / l_run;
-        half_t* dst = p.out + ((size_t)img * T + qrow) * kHidden + head * kHeadDim;
+        const int row = img * T + qrow;
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const int ch = ct * 32 + g * 8 + hi * 4;
+                const int c = head * kHeadDim + ct * 32 + g * 8 + hi * 4;
                 half4_t v = {(half_t)(o[ct][4 * g] * inv), (half_t)(o[ct][4 * g + 1] * inv),
                              (half_t)(o[ct][4 * g + 2] * inv), (half_t)(o[ct][4 * g + 3] * inv)};
-                *(half4_t*)(dst + ch) = v;
+                *(half4_t*)(p.out + frag_piece(row, c & ~7, kHidden) + (c & 7)) = v;
             }
     }
 }

@@ -66,6 +66,19 @@ __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcp
 // silu(g) = g / (1 + e^-g), with e^-g evaluated as 2^(-g * log2 e) on v_exp_f32.
 __device__ __forceinline__ float silu(float g) { return g * fast_rcp(1.0f + fast_exp2(-g * kLog2e)); }
 
+// Fragment order of an f16 activation matrix A[rows][K] (K a multiple of 16;
+// rows padded to a multiple of 32): fragment (mb, ks) holds rows 32mb ..
+// 32mb+31 and columns 16ks .. 16ks+15 as 64 lanes x 8 halfs, lane hi*32 + l
+// holding row 32mb + l, columns 16ks + 8hi .. +7 — exactly the operand a
+// lane feeds v_mfma_f32_32x32x16_f16 — and fragments are stored mb-major.
+// A GEMM then loads its activation operand straight into registers, 1 KB
+// contiguous per wave and fragment, with no LDS staging.
+// frag_piece: element offset of the 8 halfs holding columns k8 .. k8+7
+// (k8 a multiple of 8) of row m.
+__device__ __forceinline__ size_t frag_piece(int m, int k8, int K) {
+    return ((size_t)(m >> 5) * (K >> 4) + (k8 >> 4)) * 512 + (((k8 >> 3) & 1) * 32 + (m & 31)) * 8;
+}
+
 // LayerNorm statistics of one row from its six 64-column partials
 // (mean_k, M2_k): mean = avg mean_k, M2 = sum M2_k + 64 * sum (mean_k -
 // mean)^2 (Chan et al.'s pairwise combination), var = M2 / 384, eps 1e-5.

@@ -8,11 +8,14 @@ namespace {
 using gemm::Tile;
 using gemm::tiles_for;
 
+// The patch embedding stages both operands in LDS (its A operand is gathered
+// from pixels); the others take activations in fragment order straight into
+// registers, four waves stacked along M.
 using PatchTile = Tile<64, 128, 2, 2>;
-using QkvTile = Tile<128, 128, 2, 2>;
-using ResidTile = Tile<64, 128, 2, 2>;
-using SwigluTile = Tile<128, 128, 2, 2>;
-using SplitTile = Tile<64, 128, 2, 2>;
+using QkvTile = Tile<128, 128, 4, 1>;
+using ResidTile = Tile<128, 128, 4, 1>;
+using SwigluTile = Tile<128, 128, 4, 1>;
+using SplitTile = Tile<128, 128, 4, 1>;
 
 template <class T, class Args>
 hipError_t launch(void (*kernel)(Args), int tiles, const Args& a, hipStream_t s) {
@@ -36,8 +39,8 @@ hipError_t launch_qkv_rope(const QkvArgs& a, hipStream_t s) {
 
 hipError_t launch_resid(const ResidArgs& a, hipStream_t s) {
     const int tiles = tiles_for<ResidTile>(a.rows, kHidden);
-    return a.stats ? launch<ResidTile>(gemm::resid_kernel<ResidTile, true, 2>, tiles, a, s)
-                   : launch<ResidTile>(gemm::resid_kernel<ResidTile, false, 2>, tiles, a, s);
+    return a.stats ? launch<ResidTile>(gemm::resid_kernel<ResidTile, true>, tiles, a, s)
+                   : launch<ResidTile>(gemm::resid_kernel<ResidTile, false>, tiles, a, s);
 }
 
 hipError_t launch_swiglu(const SwigluArgs& a, hipStream_t s) {

@@ -38,6 +38,7 @@ struct Tile {
     static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile is a multiple of the 32x32 MFMA tile");
     static constexpr int FM = TM / 32, FN = TN / 32;
     static constexpr int STAGE_HALFS = (BM + BN) * LDK;
+    static constexpr int W_HALFS = BN * LDK;  // weight-only stage (activations in registers)
     static constexpr int LDS_HALFS = 2 * STAGE_HALFS;
     static constexpr int LDS_BYTES = LDS_HALFS * 2;
 };
@@ -89,9 +90,10 @@ struct HalfTile {
     }
 };
 
-// A operand: f16 activations [M][lda], rows m0 .. m0+BM-1.
+// A operand: f16 activations [M][lda], rows m0 .. m0+BM-1, staged in LDS.
 template <class T>
 struct ActRows {
+    static constexpr bool kInRegs = false;
     HalfTile<T::BM, T::THREADS, T::BK, T::LDK> t;
     const half_t* a;
     int lda, M, k_off;
@@ -112,6 +114,32 @@ struct WeightRows {
         t.load_all(w, ldw, n0, k_off + kt * T::BK, tid);
     }
     __device__ __forceinline__ void store(half_t* s, int tid) const { t.store(s, tid); }
+};
+
+// A operand in fragment order (common.hpp), loaded straight into the
+// registers the MFMAs read: each wave loads the fragments of its own TM rows
+// (waves split the tile along M only, so no two waves load the same data).
+// Blocks past the last one repeat it (they only feed unstored rows).
+template <class T>
+struct ActFrags {
+    static constexpr bool kInRegs = true;
+    static constexpr int KS = T::BK / 16;
+    static_assert(T::WGN == 1, "each wave owns whole rows of the tile");
+    half8_t f[T::FM][KS];
+    const half_t* a;
+    int ksteps;   // K / 16 of the whole matrix
+    int mblocks;  // 32-row blocks of the matrix
+    int ks_off;   // first k-step (split-K)
+    __device__ __forceinline__ void load(int m0, int /*n0*/, int kt, int tid) {
+        const int lane = tid & 63, wm = (tid >> 6) % T::WGM;
+#pragma unroll
+        for (int j = 0; j < T::FM; ++j) {
+            const int mb = min((m0 + wm * T::TM) / 32 + j, mblocks - 1);
+            const half_t* base = a + ((size_t)mb * ksteps + ks_off + kt * KS) * 512 + lane * 8;
+#pragma unroll
+            for (int kk = 0; kk < KS; ++kk) f[j][kk] = *(const half8_t*)(base + kk * 512);
+        }
+    }
 };
 
 template <class T>
@@ -147,6 +175,29 @@ __device__ __forceinline__ void mma_stage(const half_t* stage, int tid, Acc<T>& 
     }
 }
 
+// mma_stage with the activation fragments already in registers (ActFrags)
+// and only the weight stage in LDS.
+template <class T, class AF>
+__device__ __forceinline__ void mma_stage_areg(const half_t* stage, int tid, const AF& af, Acc<T>& acc) {
+    const int lane = tid & 63, wn = (tid >> 6) / T::WGM;
+    const int l32 = lane & 31, hi = lane >> 5;
+    const half_t* w_s = stage + (wn * T::TN + l32) * T::LDK + hi * 8;
+    half8_t wf[2][T::FN];
+    auto fetch = [&](int kk, int b) {
+#pragma unroll
+        for (int i = 0; i < T::FN; ++i) wf[b][i] = *(const half8_t*)(w_s + i * 32 * T::LDK + kk * 16);
+    };
+    fetch(0, 0);
+#pragma unroll
+    for (int kk = 0; kk < T::BK / 16; ++kk) {
+        if (kk + 1 < T::BK / 16) fetch(kk + 1, (kk + 1) & 1);
+#pragma unroll
+        for (int i = 0; i < T::FN; ++i)
+#pragma unroll
+            for (int j = 0; j < T::FM; ++j) acc.v[i][j] = mfma32x32x16(wf[kk & 1][i], af.f[j][kk], acc.v[i][j]);
+    }
+}
+
 // The workgroup's tile: hardware workgroup ids are dispatched round-robin
 // over the 8 XCDs (each with its own L2); the tile space (n fastest) is cut
 // into 8 contiguous chunks and XCD x takes chunk x, so the workgroups of one
@@ -179,29 +230,56 @@ __device__ __forceinline__ void gemm_main(AL (&al)[P], WL (&wl)[P], int m0, int 
 #pragma unroll
         for (int j = 0; j < T::FM; ++j) acc.v[i][j] = float16_t{};
     const int last = k_tiles - 1;
-#pragma unroll
-    for (int i = 0; i < P; ++i) {
-        al[i].load(m0, n0, min(i, last), tid);
-        wl[i].load(m0, n0, min(i, last), tid);
-    }
-    al[0].store(lds, tid);
-    wl[0].store(lds + T::BM * T::LDK, tid);
-    lds_barrier();
-    for (int base = 0; base < k_tiles; base += L) {
-#pragma unroll
-        for (int i = 0; i < L; ++i) {
-            const int s = base + i;
-            if (s >= k_tiles) break;  // uniform
-            half_t* const cur = lds + (i % 2) * T::STAGE_HALFS;
-            half_t* const nxt = lds + ((i + 1) % 2) * T::STAGE_HALFS;
-            al[i % P].load(m0, n0, min(s + P, last), tid);
-            wl[i % P].load(m0, n0, min(s + P, last), tid);
-            mma_stage<T>(cur, tid, acc);
-            if (s + 1 < k_tiles) {
-                al[(i + 1) % P].store(nxt, tid);
-                wl[(i + 1) % P].store(nxt + T::BM * T::LDK, tid);
-            }
+    if constexpr (AL::kInRegs) {
+        // Activations in registers, only W through LDS: register set b of
+        // both operands holds the stage computed from LDS buffer b; a set is
+        // refilled (two stages ahead) once that stage's MFMAs have read it.
+        static_assert(P == 2, "two register sets");
+        half_t* const s0 = lds;
+        half_t* const s1 = lds + T::W_HALFS;
+        al[0].load(m0, n0, 0, tid);
+        wl[0].load(m0, n0, 0, tid);
+        al[1].load(m0, n0, min(1, last), tid);
+        wl[1].load(m0, n0, min(1, last), tid);
+        wl[0].store(s0, tid);
+        lds_barrier();
+        for (int kt = 0; kt < k_tiles; kt += 2) {
+            wl[0].load(m0, n0, min(kt + 2, last), tid);
+            mma_stage_areg<T>(s0, tid, al[0], acc);
+            al[0].load(m0, n0, min(kt + 2, last), tid);
+            wl[1].store(s1, tid);
             lds_barrier();
+            wl[1].load(m0, n0, min(kt + 3, last), tid);
+            mma_stage_areg<T>(s1, tid, al[1], acc);
+            al[1].load(m0, n0, min(kt + 3, last), tid);
+            if (kt + 2 < k_tiles) wl[0].store(s0, tid);
+            lds_barrier();
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            al[i].load(m0, n0, min(i, last), tid);
+            wl[i].load(m0, n0, min(i, last), tid);
+        }
+        al[0].store(lds, tid);
+        wl[0].store(lds + T::BM * T::LDK, tid);
+        lds_barrier();
+        for (int base = 0; base < k_tiles; base += L) {
+#pragma unroll
+            for (int i = 0; i < L; ++i) {
+                const int s = base + i;
+                if (s >= k_tiles) break;  // uniform
+                half_t* const cur = lds + (i % 2) * T::STAGE_HALFS;
+                half_t* const nxt = lds + ((i + 1) % 2) * T::STAGE_HALFS;
+                al[i % P].load(m0, n0, min(s + P, last), tid);
+                wl[i % P].load(m0, n0, min(s + P, last), tid);
+                mma_stage<T>(cur, tid, acc);
+                if (s + 1 < k_tiles) {
+                    al[(i + 1) % P].store(nxt, tid);
+                    wl[(i + 1) % P].store(nxt + T::BM * T::LDK, tid);
+                }
+                lds_barrier();
+            }
         }
     }
 }

@@ -4,6 +4,11 @@
 // with the embed scatter of kernels/embed_scatter_f32.loom fused in),
 // matmul_qkv_rope_f16_wmma.loom, matmul_resid_f16_wmma.loom,
 // matmul_swiglu_f16_wmma.loom and matmul_splitk_f16_wmma.loom.
+//
+// Activations (x, h, attn, act) are kept in fragment order (common.hpp):
+// every GEMM except the patch embedding loads its activation operand
+// straight into registers (ActFrags) and stages only the weights in LDS,
+// with the workgroup's waves stacked along M (32 x 128 per wave).
 #pragma once
 #include "gemm_core.hpp"
 #include "launch.hpp"
@@ -19,6 +24,7 @@ namespace gemm {
 // on the way to LDS.
 template <class T>
 struct PatchRows {
+    static constexpr bool kInRegs = false;
     static_assert(T::BK == 64, "a stage is one channel x four pixel rows");
     static constexpr int CHUNKS = T::BM * T::BK / 4 / T::THREADS;
     static_assert(T::BM * T::BK / 4 % T::THREADS == 0, "patch tile splits evenly");
@@ -46,33 +52,30 @@ struct PatchRows {
     }
 };
 
-// Writes the (mean, M2) partial of row m over the 64 columns of one
-// statistics slot, whose values are spread over 8 consecutive lanes (8 each,
-// already rounded to the f16 values stored in x). All 8 lanes must call this.
-__device__ __forceinline__ void slot_stats(float* stats, size_t m, int slot, const float (&v)[8], int lane8) {
-    float s = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
-    s += __shfl_xor(s, 4, 64);
+// (mean, M2) partial of one row over a 64-column statistics slot whose
+// values are split between this lane (32 of them, already rounded to the f16
+// values stored in x) and its partner lane l ^ 32. Both partners call this;
+// the lane with hi == 0 writes.
+__device__ __forceinline__ void pair_stats(float* stats, size_t m, int slot, const float (&v)[32], int hi, bool store) {
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < 32; ++e) s += v[e];
+    s += __shfl_xor(s, 32, 64);
     const float mean = s * (1.0f / 64.0f);
     float q = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) q += (v[e] - mean) * (v[e] - mean);
-    q += __shfl_xor(q, 1, 64);
-    q += __shfl_xor(q, 2, 64);
-    q += __shfl_xor(q, 4, 64);
-    if (lane8 == 0) *(float2_t*)(stats + m * kStatFloats + slot * 2) = float2_t{mean, q};
+    for (int e = 0; e < 32; ++e) q += (v[e] - mean) * (v[e] - mean);
+    q += __shfl_xor(q, 32, 64);
+    if (store && hi == 0) *(float2_t*)(stats + m * kStatFloats + slot * 2) = float2_t{mean, q};
 }
 
-__device__ __forceinline__ float4_t widen(half4_t h) { return float4_t{(float)h[0], (float)h[1], (float)h[2], (float)h[3]}; }
-
 // Patch embedding + CLS/register scatter into the f16 residual stream x
-// (with STATS, also the LayerNorm row statistics of x). Each wave rounds its
-// 32 x 64 block to f16 into LDS, then writes it as 128-byte row pieces
-// (8 lanes per row), which is also the layout the row statistics need.
+// (fragment order; with STATS, also the LayerNorm row statistics of x). Each
+// wave rounds its 32 x 64 block to f16 into LDS, then writes it as fragment
+// pieces, lane (l, hi) taking row l and the half hi of each 16-column block.
 template <class T, bool STATS>
 __global__ __launch_bounds__(T::THREADS) void patch_embed_kernel(PatchEmbedArgs p) {
-    static_assert(T::TN == 64, "one statistics slot per wave");
+    static_assert(T::TN == 64 && T::TM == 32, "one 32-row block and one statistics slot per wave");
     constexpr int SP = T::TN + 8;  // staging pitch in halfs
     static_assert(T::WAVES * T::TM * SP <= T::LDS_HALFS, "staging fits the stage buffers");
     __shared__ __attribute__((aligned(16))) half_t lds[T::LDS_HALFS];
@@ -90,139 +93,135 @@ __global__ __launch_bounds__(T::THREADS) void patch_embed_kernel(PatchEmbedArgs 
             for (int g = 0; g < 4; ++g) {
                 const int n = f.col(i, g);
                 const float4_t b = ld4(p.bias + n);
-#pragma unroll
-                for (int j = 0; j < T::FM; ++j)
-                    *(half4_t*)(st + (j * 32 + f.l32) * SP + (n - f.n_base)) = to_half4(group4(acc.v[i][j], g) + b);
+                *(half4_t*)(st + f.l32 * SP + (n - f.n_base)) = to_half4(group4(acc.v[i][0], g) + b);
             }
         wave_lds_sync();
-        const int lane = threadIdx.x & 63, r0 = lane >> 3, c8 = (lane & 7) * 8;
+        const int m = f.m_base + f.l32;
+        const bool valid = m < M;
+        const size_t row = valid ? (size_t)m + (size_t)(m / P + 1) * kPrefix : 0;  // image*Tok + kPrefix + patch
+        float v[32];
 #pragma unroll
-        for (int it = 0; it < T::TM / 8; ++it) {
-            const int r = it * 8 + r0, m = f.m_base + r;
-            if (m >= M) continue;  // uniform over the 8 lanes of a row
-            const size_t row = (size_t)m + (size_t)(m / P + 1) * kPrefix;  // image*Tok + kPrefix + patch
-            const half8_t h = *(const half8_t*)(st + r * SP + c8);
-            *(half8_t*)(p.x + row * kHidden + f.n_base + c8) = h;
-            if constexpr (STATS) {
-                float v[8];
+        for (int ks = 0; ks < 4; ++ks) {
+            const half8_t h = *(const half8_t*)(st + f.l32 * SP + ks * 16 + f.hi * 8);
+            if (valid) *(half8_t*)(p.x + frag_piece((int)row, f.n_base + ks * 16 + f.hi * 8, kHidden)) = h;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) v[e] = (float)h[e];
-                slot_stats(p.stats, row, f.n_base / 64, v, lane & 7);
-            }
+            for (int e = 0; e < 8; ++e) v[ks * 8 + e] = (float)h[e];
         }
+        if constexpr (STATS) pair_stats(p.stats, row, f.n_base / 64, v, f.hi, valid);
         // CLS + registers of every image whose first patch row lies in this tile.
         const int m_end = min(m0 + T::BM, M);
         for (int img = (m0 + P - 1) / P; img * P < m_end; ++img) {
             for (int idx = threadIdx.x; idx < kPrefix * T::BN; idx += T::THREADS) {
-                const int row = idx / T::BN, col = n0 + idx % T::BN;
-                p.x[((size_t)img * Tok + row) * kHidden + col] = (half_t)p.prefix[row * kHidden + col];
+                const int r = idx / T::BN, col = n0 + idx % T::BN;
+                p.x[frag_piece(img * Tok + r, col & ~7, kHidden) + (col & 7)] = (half_t)p.prefix[r * kHidden + col];
             }
             if constexpr (STATS) {
                 constexpr int slots = T::BN / 64;
                 for (int idx = threadIdx.x; idx < kPrefix * slots * 2; idx += T::THREADS) {
-                    const int row = idx / (slots * 2), e = idx % (slots * 2);
+                    const int r = idx / (slots * 2), e = idx % (slots * 2);
                     const int off = (n0 / 64) * 2 + e;
-                    p.stats[((size_t)img * Tok + row) * kStatFloats + off] = p.prefix_stats[row * kStatFloats + off];
+                    p.stats[((size_t)img * Tok + r) * kStatFloats + off] = p.prefix_stats[r * kStatFloats + off];
                 }
             }
         }
     });
 }
 
-// QKV + bias + 2D RoPE. A wave's 64 columns are exactly one head of q, k or
-// v, so channel c and its rotation partner c+32 are acc.v[0] / acc.v[1] of
-// the same lane, and both use angle column c of the RoPE tables (DINOv3's
-// tables repeat columns 0..31 in 32..63; only the first half is read).
-// Results are rounded to f16 into a per-wave LDS block, then each wave
-// writes its rows as whole 128-byte head rows: q, k and v are all
-// head-major [image][head][tpad][64], and the rows of one image are
-// contiguous there.
+template <class T>
+__device__ __forceinline__ void init_frags(ActFrags<T> (&al)[2], const half_t* a, int rows, int k, int ks_off = 0) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        al[i].a = a;
+        al[i].ksteps = k / 16;
+        al[i].mblocks = (rows + 31) / 32;
+        al[i].ks_off = ks_off;
+    }
+}
+
+// QKV + bias + 2D RoPE. A wave's 128 columns are two heads of q, k or v (a
+// 128-column tile never straddles two of them); channel c and its rotation
+// partner c+32 of a head are acc.v[2h] / acc.v[2h+1] of the same lane, and
+// both use angle column c of the RoPE tables (DINOv3's tables repeat columns
+// 0..31 in 32..63; only the first half is read). Results are rounded to f16
+// into a per-wave LDS block, then written as whole 128-byte head rows:
+// q, k and v are all head-major [image][head][tpad][64], and the rows of one
+// image are contiguous there.
 template <class T, bool LN>
-__global__ __launch_bounds__(T::THREADS) void qkv_rope_kernel(QkvArgs p) {
-    static_assert(T::TN == kHeadDim, "one head per wave");
-    constexpr int SP = kHeadDim + 8;  // staging pitch in halfs
-    static_assert(T::WAVES * T::TM * SP <= T::LDS_HALFS, "staging fits the stage buffers");
-    __shared__ __attribute__((aligned(16))) half_t lds[T::LDS_HALFS];
+__global__ __launch_bounds__(T::THREADS, 3) void qkv_rope_kernel(QkvArgs p) {
+    static_assert(T::TN == 2 * kHeadDim && T::TM == 32, "two heads per wave");
+    constexpr int SP = T::TN + 8;  // staging pitch in halfs
+    constexpr int LDS = T::WAVES * T::TM * SP > 2 * T::W_HALFS ? T::WAVES * T::TM * SP : 2 * T::W_HALFS;
+    __shared__ __attribute__((aligned(16))) half_t lds[LDS];
     const int P = p.grid * p.grid, Tok = P + kPrefix, M = p.images * Tok;
     constexpr int NT = 3 * kHidden / T::BN;
-    ActRows<T> al[2] = {{{}, p.h, kHidden, M, 0}, {{}, p.h, kHidden, M, 0}};
+    ActFrags<T> al[2];
+    init_frags(al, p.h, M, kHidden);
     WeightRows<T> wl[2] = {{{}, p.w, kHidden, 0}, {{}, p.w, kHidden, 0}};
     gemm_tile<T>(al, wl, NT, NT * ((M + T::BM - 1) / T::BM), kHidden / T::BK, lds, [&](const Acc<T>& acc, int m0, int n0) {
         const Frag<T> f(m0, n0);
         const int lane = threadIdx.x & 63;
         half_t* const st = lds + (threadIdx.x >> 6) * (T::TM * SP);
-        const int part = f.n_base / kHidden, head = (f.n_base % kHidden) / kHeadDim;
-        float4_t bias[2][4], wsum[2][4];
+        const int part = f.n_base / kHidden, head0 = (f.n_base % kHidden) / kHeadDim;
+        const int m = min(f.m_base + f.l32, M - 1);  // rows past M are computed but never written out
+        const int tok = m % Tok;
+        // RoPE angles of this row, gathered together before any use (lanes
+        // hold different rows); prefix rows and v rotate by cos 1, sin 0.
+        const size_t angle_row = (size_t)max(tok - kPrefix, 0) * kHeadDim;
+        float4_t co[4], si[4];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            const int c = g * 8 + f.hi * 4;
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                bias[i][g] = ld4(p.bias + f.n_base + 32 * i + c);
-                if constexpr (LN) wsum[i][g] = ld4(p.wsum + f.n_base + 32 * i + c);
+            co[g] = float4_t{1.f, 1.f, 1.f, 1.f};
+            si[g] = float4_t{};
+            if (part < 2) {  // uniform per wave
+                co[g] = ld4(p.cos + angle_row + g * 8 + f.hi * 4);
+                si[g] = ld4(p.sin + angle_row + g * 8 + f.hi * 4);
             }
         }
-        const bool rope_part = part < 2;  // uniform per wave
-#pragma unroll
-        for (int j = 0; j < T::FM; ++j) {
-            const int m = min(f.row(j), M - 1);  // rows past M are computed but never written out
-            const int tok = m % Tok;
-            // RoPE angles of this row, loaded together before any use (lanes
-            // hold different rows, so each load is a gather; one round trip
-            // per row instead of one per register group). Prefix rows and v
-            // columns rotate by cos 1, sin 0.
-            const size_t angle_row = (size_t)max(tok - kPrefix, 0) * kHeadDim;
-            float4_t co[4], si[4];
+        if (tok < kPrefix) {
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 co[g] = float4_t{1.f, 1.f, 1.f, 1.f};
                 si[g] = float4_t{};
-                if (rope_part) {
-                    co[g] = ld4(p.cos + angle_row + g * 8 + f.hi * 4);
-                    si[g] = ld4(p.sin + angle_row + g * 8 + f.hi * 4);
-                }
             }
-            if (tok < kPrefix) {
+        }
+        RowNorm rn{0.f, 1.f};
+        if constexpr (LN) rn = row_norm(p.stats, m);
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    co[g] = float4_t{1.f, 1.f, 1.f, 1.f};
-                    si[g] = float4_t{};
-                }
-            }
-            RowNorm rn{0.f, 1.f};
-            if constexpr (LN) rn = row_norm(p.stats, m);
-            half_t* const row = st + (j * 32 + f.l32) * SP;
+        for (int h2 = 0; h2 < 2; ++h2)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int c = g * 8 + f.hi * 4;  // channel in the head (0..31); partner c + 32
-                float4_t lo = group4(acc.v[0][j], g), up = group4(acc.v[1][j], g);
+                const int n = f.n_base + h2 * kHeadDim + c;
+                float4_t lo = group4(acc.v[2 * h2][0], g), up = group4(acc.v[2 * h2 + 1][0], g);
                 if constexpr (LN) {
-                    lo = (lo - rn.mean * wsum[0][g]) * rn.rstd;
-                    up = (up - rn.mean * wsum[1][g]) * rn.rstd;
+                    lo = (lo - rn.mean * ld4(p.wsum + n)) * rn.rstd;
+                    up = (up - rn.mean * ld4(p.wsum + n + 32)) * rn.rstd;
                 }
-                lo += bias[0][g];
-                up += bias[1][g];
+                lo += ld4(p.bias + n);
+                up += ld4(p.bias + n + 32);
                 const float4_t nlo = lo * co[g] - up * si[g];  // x[c] cos - x[c+32] sin
                 const float4_t nup = up * co[g] + lo * si[g];  // x[c+32] cos + x[c] sin
-                *(half4_t*)(row + c) = to_half4(nlo);
-                *(half4_t*)(row + 32 + c) = to_half4(nup);
+                *(half4_t*)(st + f.l32 * SP + h2 * kHeadDim + c) = to_half4(nlo);
+                *(half4_t*)(st + f.l32 * SP + h2 * kHeadDim + 32 + c) = to_half4(nup);
             }
-        }
         wave_lds_sync();
-        // Copy-out: 8 lanes per 128-byte row, 8 rows per pass.
+        // Copy-out: 8 lanes per 128-byte head row, 8 rows per pass.
         half_t* const out = part == 0 ? p.q : part == 1 ? p.k : p.v;
         const int r0 = lane >> 3, ch = (lane & 7) * 8;
-        int m = f.m_base + r0;
-        int img = m / Tok, tok = m - img * Tok;
+        int mr = f.m_base + r0;
+        int img = mr / Tok, t = mr - img * Tok;
 #pragma unroll
         for (int it = 0; it < T::TM / 8; ++it) {
-            if (m < M)
-                *(half8_t*)(out + (((size_t)img * kHeads + head) * p.tpad + tok) * kHeadDim + ch) =
-                    *(const half8_t*)(st + (it * 8 + r0) * SP + ch);
-            m += 8;
-            tok += 8;
-            while (tok >= Tok) {
-                tok -= Tok;
+            if (mr < M) {
+#pragma unroll
+                for (int h2 = 0; h2 < 2; ++h2)
+                    *(half8_t*)(out + (((size_t)img * kHeads + head0 + h2) * p.tpad + t) * kHeadDim + ch) =
+                        *(const half8_t*)(st + (it * 8 + r0) * SP + h2 * kHeadDim + ch);
+            }
+            mr += 8;
+            t += 8;
+            while (t >= Tok) {
+                t -= Tok;
                 ++img;
             }
         }
@@ -230,25 +229,19 @@ __global__ __launch_bounds__(T::THREADS) void qkv_rope_kernel(QkvArgs p) {
 }
 
 // Residual GEMM: x += ls * (A W^T + b), in place on the f16 residual stream
-// (with STATS, also the LayerNorm row statistics of the updated x); P
-// register sets in the K loop (a third set measured no faster, even for the
-// K = 1536 down projection). Each wave
-// stages its f32 update (32 x 64) in LDS, then reads and writes x as
-// 128-byte row pieces, 8 lanes per row.
-template <class T, bool STATS, int P>
+// in fragment order (with STATS, also the LayerNorm row statistics of the
+// updated x). Each wave stages its f32 update (32 x 128) in LDS, then reads
+// and writes x fragment by fragment (1 KB contiguous per wave access).
+template <class T, bool STATS>
 __global__ __launch_bounds__(T::THREADS) void resid_kernel(ResidArgs p) {
-    static_assert(T::TN == 64, "one statistics slot per wave");
+    static_assert(T::TN == 128 && T::TM == 32, "two statistics slots per wave");
     constexpr int SPF = T::TN + 4;  // staging pitch in floats
-    static_assert(T::WAVES * T::TM * SPF * 4 <= T::LDS_BYTES, "staging fits the stage buffers");
-    __shared__ __attribute__((aligned(16))) half_t lds[T::LDS_HALFS];
+    constexpr int LDS = T::WAVES * T::TM * SPF * 2 > 2 * T::W_HALFS ? T::WAVES * T::TM * SPF * 2 : 2 * T::W_HALFS;
+    __shared__ __attribute__((aligned(16))) half_t lds[LDS];
     constexpr int NT = kHidden / T::BN;
-    ActRows<T> al[P];
-    WeightRows<T> wl[P];
-#pragma unroll
-    for (int i = 0; i < P; ++i) {
-        al[i] = ActRows<T>{{}, p.a, p.k, p.rows, 0};
-        wl[i] = WeightRows<T>{{}, p.w, p.k, 0};
-    }
+    ActFrags<T> al[2];
+    init_frags(al, p.a, p.rows, p.k);
+    WeightRows<T> wl[2] = {{{}, p.w, p.k, 0}, {{}, p.w, p.k, 0}};
     gemm_tile<T>(al, wl, NT, NT * ((p.rows + T::BM - 1) / T::BM), p.k / T::BK, lds,
                        [&](const Acc<T>& acc, int m0, int n0) {
         const Frag<T> f(m0, n0);
@@ -259,96 +252,85 @@ __global__ __launch_bounds__(T::THREADS) void resid_kernel(ResidArgs p) {
             for (int g = 0; g < 4; ++g) {
                 const int n = f.col(i, g);
                 const float4_t b = ld4(p.bias + n), l = ld4(p.ls + n);
-#pragma unroll
-                for (int j = 0; j < T::FM; ++j)
-                    *(float4_t*)(st + (j * 32 + f.l32) * SPF + (n - f.n_base)) = (group4(acc.v[i][j], g) + b) * l;
+                *(float4_t*)(st + f.l32 * SPF + (n - f.n_base)) = (group4(acc.v[i][0], g) + b) * l;
             }
         wave_lds_sync();
-        const int lane = threadIdx.x & 63, r0 = lane >> 3, c8 = (lane & 7) * 8;
+        const int mb = f.m_base / 32;
+        if (mb >= (p.rows + 31) / 32) return;  // uniform per wave
+        const int m = f.m_base + f.l32;
+        const bool valid = m < p.rows;
+        const int lane = threadIdx.x & 63;
 #pragma unroll
-        for (int it = 0; it < T::TM / 8; ++it) {
-            const int r = it * 8 + r0, m = f.m_base + r;
-            if (m >= p.rows) continue;  // uniform over the 8 lanes of a row
-            half_t* const xr = p.x + (size_t)m * kHidden + f.n_base + c8;
-            const half8_t old = *(const half8_t*)xr;
-            const float4_t u0 = *(const float4_t*)(st + r * SPF + c8), u1 = *(const float4_t*)(st + r * SPF + c8 + 4);
-            half8_t h;
-            float v[8];
+        for (int s2 = 0; s2 < 2; ++s2) {
+            float v[32];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                h[e] = (half_t)((float)old[e] + u0[e]);
-                h[e + 4] = (half_t)((float)old[e + 4] + u1[e]);
+            for (int kk = 0; kk < 4; ++kk) {
+                const int c = s2 * 64 + kk * 16 + f.hi * 8;  // column in the wave's 128
+                half_t* const xp = p.x + ((size_t)mb * (kHidden / 16) + (f.n_base + c) / 16) * 512 + lane * 8;
+                const half8_t old = *(const half8_t*)xp;
+                const float4_t u0 = *(const float4_t*)(st + f.l32 * SPF + c), u1 = *(const float4_t*)(st + f.l32 * SPF + c + 4);
+                half8_t h;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    h[e] = (half_t)((float)old[e] + u0[e]);
+                    h[e + 4] = (half_t)((float)old[e + 4] + u1[e]);
+                }
+                if (valid) *(half8_t*)xp = h;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[kk * 8 + e] = (float)h[e];
             }
-            *(half8_t*)xr = h;
-            if constexpr (STATS) {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) v[e] = (float)h[e];
-                slot_stats(p.stats, m, f.n_base / 64, v, lane & 7);
-            }
+            if constexpr (STATS) pair_stats(p.stats, m, f.n_base / 64 + s2, v, f.hi, valid);
         }
     });
 }
 
 // SwiGLU dual GEMM. W rows are packed as blocks of 32 gate rows followed by
-// the 32 matching up rows, so a wave's 64 columns are 32 gate and 32 up
-// columns of the same 32 outputs. The workgroup's BM x BN/2 block of act is
-// staged in LDS and written as whole row pieces of BN bytes.
+// the 32 matching up rows, so a wave's 128 columns are two gate/up pairs of
+// 32 outputs each. Each wave stages its 32 x 64 block of act in LDS and
+// writes it as four whole fragments (act is in fragment order).
 template <class T, bool LN>
-__global__ __launch_bounds__(T::THREADS) void swiglu_kernel(SwigluArgs p) {
-    static_assert(T::TN % 64 == 0, "whole gate/up pairs per wave");
-    constexpr int OW = T::BN / 2;   // act columns per workgroup
-    constexpr int SP = OW + 8;      // staging pitch in halfs
-    constexpr int LPR = OW / 8;     // lanes per row in the copy-out
-    static_assert(T::BM * SP <= T::LDS_HALFS && T::THREADS % LPR == 0, "staging fits the stage buffers");
-    __shared__ __attribute__((aligned(16))) half_t lds[T::LDS_HALFS];
+__global__ __launch_bounds__(T::THREADS, 3) void swiglu_kernel(SwigluArgs p) {
+    static_assert(T::TN % 64 == 0 && T::TM == 32 && T::WGN == 1, "whole gate/up pairs, one 32-row block per wave");
+    constexpr int OW = T::TN / 2;  // act columns per wave
+    constexpr int SP = OW + 8;     // staging pitch in halfs
+    constexpr int LDS = T::WAVES * T::TM * SP > 2 * T::W_HALFS ? T::WAVES * T::TM * SP : 2 * T::W_HALFS;
+    __shared__ __attribute__((aligned(16))) half_t lds[LDS];
     constexpr int NT = 2 * kFF / T::BN;
-    ActRows<T> al[2] = {{{}, p.h, kHidden, p.rows, 0}, {{}, p.h, kHidden, p.rows, 0}};
+    ActFrags<T> al[2];
+    init_frags(al, p.h, p.rows, kHidden);
     WeightRows<T> wl[2] = {{{}, p.w, kHidden, 0}, {{}, p.w, kHidden, 0}};
     gemm_tile<T>(al, wl, NT, NT * ((p.rows + T::BM - 1) / T::BM), kHidden / T::BK, lds,
                        [&](const Acc<T>& acc, int m0, int n0) {
         const Frag<T> f(m0, n0);
-        const int wave = threadIdx.x >> 6;
-        half_t* const st = lds + (wave % T::WGM) * T::TM * SP + (wave / T::WGM) * (T::TN / 2);
-        RowNorm rn[T::FM];
-#pragma unroll
-        for (int j = 0; j < T::FM; ++j) {
-            rn[j] = RowNorm{0.f, 1.f};
-            if constexpr (LN) rn[j] = row_norm(p.stats, min(f.row(j), p.rows - 1));
-        }
+        half_t* const st = lds + (threadIdx.x >> 6) * T::TM * SP;
+        RowNorm rn{0.f, 1.f};
+        if constexpr (LN) rn = row_norm(p.stats, min(f.row(0), p.rows - 1));
         // Pair q of the wave: gate = acc.v[2q], up = acc.v[2q + 1], outputs
-        // 32q .. 32q+31 of the wave's TN/2. Column constants are loaded per
+        // 32q .. 32q+31 of the wave's OW. Column constants are loaded per
         // register group to keep the register footprint small next to acc.
 #pragma unroll
         for (int q = 0; q < T::FN / 2; ++q)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int c = g * 8 + f.hi * 4, n = f.n_base + 64 * q + c;
-                const float4_t bg = ld4(p.bias + n), bu = ld4(p.bias + n + 32);
-                float4_t wg{}, wu{};
+                float4_t gate = group4(acc.v[2 * q][0], g), up = group4(acc.v[2 * q + 1][0], g);
                 if constexpr (LN) {
-                    wg = ld4(p.wsum + n);
-                    wu = ld4(p.wsum + n + 32);
+                    gate = (gate - rn.mean * ld4(p.wsum + n)) * rn.rstd;
+                    up = (up - rn.mean * ld4(p.wsum + n + 32)) * rn.rstd;
                 }
-#pragma unroll
-                for (int j = 0; j < T::FM; ++j) {
-                    float4_t gate = group4(acc.v[2 * q][j], g), up = group4(acc.v[2 * q + 1][j], g);
-                    if constexpr (LN) {
-                        gate = (gate - rn[j].mean * wg) * rn[j].rstd;
-                        up = (up - rn[j].mean * wu) * rn[j].rstd;
-                    }
-                    gate += bg;
-                    up += bu;
-                    const float4_t y = float4_t{silu(gate[0]), silu(gate[1]), silu(gate[2]), silu(gate[3])} * up;
-                    *(half4_t*)(st + (j * 32 + f.l32) * SP + 32 * q + c) = to_half4(y);
-                }
+                gate += ld4(p.bias + n);
+                up += ld4(p.bias + n + 32);
+                const float4_t y = float4_t{silu(gate[0]), silu(gate[1]), silu(gate[2]), silu(gate[3])} * up;
+                *(half4_t*)(st + f.l32 * SP + 32 * q + c) = to_half4(y);
             }
-        lds_barrier();
-        const int r0 = threadIdx.x / LPR, c8 = (threadIdx.x % LPR) * 8;
+        wave_lds_sync();
+        const int mb = f.m_base / 32;
+        if (mb >= (p.rows + 31) / 32) return;  // uniform per wave
+        const int lane = threadIdx.x & 63;
 #pragma unroll
-        for (int it = 0; it < T::BM * LPR / T::THREADS; ++it) {
-            const int r = it * (T::THREADS / LPR) + r0, m = m0 + r;
-            if (m < p.rows) *(half8_t*)(p.act + (size_t)m * kFF + n0 / 2 + c8) = *(const half8_t*)(lds + r * SP + c8);
-        }
+        for (int ks = 0; ks < OW / 16; ++ks)
+            *(half8_t*)(p.act + ((size_t)mb * (kFF / 16) + f.n_base / 32 + ks) * 512 + lane * 8) =
+                *(const half8_t*)(st + f.l32 * SP + ks * 16 + f.hi * 8);
     });
 }
 
@@ -364,14 +346,12 @@ struct SplitDecode {
 };
 
 template <class T>
-struct SplitActRows {
-    ActRows<T> a;
+struct SplitActFrags : ActFrags<T> {
     SplitDecode<T> d;
     __device__ __forceinline__ void load(int m0, int n0, int kt, int tid) {
-        a.k_off = d.split(m0) * d.kc;
-        a.load(d.row0(m0), n0, kt, tid);
+        this->ks_off = d.split(m0) * (d.kc / 16);
+        ActFrags<T>::load(d.row0(m0), n0, kt, tid);
     }
-    __device__ __forceinline__ void store(half_t* s, int tid) const { a.store(s, tid); }
 };
 
 template <class T>
@@ -386,26 +366,25 @@ struct SplitWeightRows {
 };
 
 template <class T>
-__global__ __launch_bounds__(T::THREADS) void splitk_kernel(SplitKArgs p) {
-    __shared__ __attribute__((aligned(16))) half_t lds[T::LDS_HALFS];
+__global__ __launch_bounds__(T::THREADS, 3) void splitk_kernel(SplitKArgs p) {
+    __shared__ __attribute__((aligned(16))) half_t lds[2 * T::W_HALFS];
     constexpr int NT = kHidden / T::BN;
     const int MT = (p.rows + T::BM - 1) / T::BM;
     const SplitDecode<T> d{MT, p.k / p.splits};
-    SplitActRows<T> al[2] = {{{{}, p.a, p.k, p.rows, 0}, d}, {{{}, p.a, p.k, p.rows, 0}, d}};
+    ActFrags<T> base[2];
+    init_frags(base, p.a, p.rows, p.k);
+    SplitActFrags<T> al[2] = {{base[0], d}, {base[1], d}};
     SplitWeightRows<T> wl[2] = {{{{}, p.w, p.k, 0}, d}, {{{}, p.w, p.k, 0}, d}};
     gemm_tile<T>(al, wl, NT, NT * MT * p.splits, d.kc / T::BK, lds, [&](const Acc<T>& acc, int m0, int n0) {
         const Frag<T> f(d.row0(m0), n0);
         float* slab = p.partials + (size_t)d.split(m0) * p.rows * kHidden;
+        const int m = f.row(0);
+        if (m >= p.rows) return;
 #pragma unroll
-        for (int j = 0; j < T::FM; ++j) {
-            const int m = f.row(j);
-            if (m >= p.rows) continue;
+        for (int i = 0; i < T::FN; ++i)
 #pragma unroll
-            for (int i = 0; i < T::FN; ++i)
-#pragma unroll
-                for (int g = 0; g < 4; ++g)
-                    *(float4_t*)(slab + (size_t)m * kHidden + f.col(i, g)) = group4(acc.v[i][j], g);
-        }
+            for (int g = 0; g < 4; ++g)
+                *(float4_t*)(slab + (size_t)m * kHidden + f.col(i, g)) = group4(acc.v[i][0], g);
     });
 }
 

@@ -1,6 +1,10 @@
 // Host-side launchers for the forward-pass kernels. Each launcher assumes the
 // engine has already checked every binding's size against the shapes below
 // (engine.cpp: required_bytes); they only derive grids and launch.
+//
+// The f16 activations x, h, attn and act are stored in fragment order
+// (common.hpp: frag_piece), rows padded to a multiple of 32; "[rows][K] frag"
+// below means that layout.
 #pragma once
 #include <hip/hip_runtime.h>
 #include "common.hpp"
@@ -8,7 +12,8 @@
 namespace dhx {
 
 // Row LayerNorm over 384 channels, eps 1e-5, fp32 statistics.
-// x [rows][384] f16 -> out [rows][384] f16 (or f32 when f32_out).
+// x [rows][384] frag -> out [rows][384] frag f16 (or row-major f32 when
+// f32_out).
 struct LayerNormArgs {
     const half_t* x;
     const float* gamma;
@@ -20,8 +25,8 @@ struct LayerNormArgs {
 
 // Fused patch embedding: im2col of NCHW f32 pixels (patch order (gy, gx),
 // k order (c, dy, dx)), GEMM with patch_w [384][768] f16, + bias, narrowed to
-// f16 and scattered into x [images*T][384] after the CLS + 4 register rows,
-// which are copied from prefix [5][384] f32.
+// f16 and scattered into x [images*T][384] frag after the CLS + 4 register
+// rows, which are copied from prefix [5][384] f32.
 struct PatchEmbedArgs {
     const float* pixels;
     const half_t* w;
@@ -44,7 +49,7 @@ struct PatchEmbedArgs {
 constexpr int kStatSlots = kHidden / 64;
 constexpr int kStatFloats = 2 * kStatSlots;
 
-// h [rows][384] f16 . Wqkv[1152][384]^T + b, 2D RoPE on q and k of patch
+// h [rows][384] frag . Wqkv[1152][384]^T + b, 2D RoPE on q and k of patch
 // tokens, written head-major: q, k, v [images][6][tpad][64] (rows past the
 // image's tokens are never written). cos / sin are [patches][64] with columns
 // 32..63 repeating 0..31 (the rotation of channels c and c+32 uses angle c);
@@ -72,7 +77,7 @@ struct QkvArgs {
 // softmax(q k^T / 8) v per (image, head) over that image's T tokens, with
 // q, k, v as written by the QKV kernel; rows T .. tpad-1 of v must be finite
 // (the engine zeroes buffers at allocation and nothing writes those rows).
-// out [images*T][384] f16 (head h in columns 64h .. 64h+63).
+// out [images*T][384] frag (head h in columns 64h .. 64h+63).
 struct AttentionArgs {
     const half_t* q;
     const half_t* k;
@@ -83,7 +88,8 @@ struct AttentionArgs {
     int tpad;
 };
 
-// x[rows][384] += ls * (a[rows][k] . W[384][k]^T + b), f16 residual in place.
+// x[rows][384] += ls * (a[rows][k] . W[384][k]^T + b), f16 residual in place
+// (a and x frag).
 struct ResidArgs {
     const half_t* a;
     const half_t* w;
@@ -95,7 +101,7 @@ struct ResidArgs {
     float* stats = nullptr;  // optional: row statistics of the updated x
 };
 
-// act[rows][1536] = silu(h.Wg^T + bg) * (h.Wu^T + bu); W and b are packed
+// act[rows][1536] frag = silu(h.Wg^T + bg) * (h.Wu^T + bu), h frag; W and b are packed
 // with gate and up rows interleaved in blocks of 32.
 // stats / wsum: LayerNorm fused as in QkvArgs.
 struct SwigluArgs {
@@ -108,7 +114,8 @@ struct SwigluArgs {
     const float* wsum = nullptr;
 };
 
-// partials[s][rows][384] = a[:, s*k/splits ...] . W[:, s*k/splits ...]^T (f32).
+// partials[s][rows][384] = a[:, s*k/splits ...] . W[:, s*k/splits ...]^T
+// (f32 row-major; a frag).
 struct SplitKArgs {
     const half_t* a;
     const half_t* w;
@@ -118,7 +125,7 @@ struct SplitKArgs {
     int splits;
 };
 
-// x[rows][384] += ls * (sum_s partials[s] + b).
+// x[rows][384] frag += ls * (sum_s partials[s] + b).
 struct ReduceArgs {
     const float* partials;
     const float* bias;

@@ -119,13 +119,16 @@ public:
         }
         const uint64_t B = opts.max_batch, r = B * tokens_;
         const uint64_t heads = B * 6 * tpad_ * 64 * 2;
-        // x, h, attn and act are f16; q/k/v are f16 head-major (padded rows
+        // Activations in fragment order: each image group starts on a 32-row
+        // block, so up to 32 padding rows per group.
+        const uint64_t rf = r + 32ull * DHX_MAX_BRANCHES;
+        // x, h, attn and act are f16 in fragment order; q/k/v are f16 head-major (padded rows
         // stay zero); out, the NCHW images, the split-K slabs and the
         // LayerNorm row statistics of x are f32. The images and out exist
         // twice (one per transfer slot) so that consecutive chunks of a
         // forward overlap their uploads and readbacks with each other's graph.
-        const uint64_t sizes[kBuffers] = {r * kHiddenU * 2, r * kHiddenU * 2, heads, heads, heads, r * kHiddenU * 2,
-                                          r * 1536 * 2,     r * kHiddenU * 4, B * image_elems_ * 4,
+        const uint64_t sizes[kBuffers] = {rf * kHiddenU * 2, rf * kHiddenU * 2, heads, heads, heads, rf * kHiddenU * 2,
+                                          rf * 1536 * 2,     r * kHiddenU * 4, B * image_elems_ * 4,
                                           (uint64_t)kSplits * r * kHiddenU * 4, r * 12 * 4,
                                           r * kHiddenU * 4, B * image_elems_ * 4};
         for (int i = 0; i < kBuffers; ++i) check(dhx_allocate(e, sizes[i], &a_[i]), e);
@@ -224,17 +227,20 @@ public:
         const uint32_t nb = groups(b);
         std::vector<dhx_launch> l;
         std::vector<uint64_t> counts;
+        uint64_t frag_row0 = 0;  // first 32-row block of the group in the fragment-order buffers
         for (uint32_t g = 0; g < nb; ++g) {
             const uint64_t first = b * g / nb, end = b * (g + 1) / nb;
             const size_t before = l.size();
-            plan(first, end - first, b, slot, l);
+            plan(first, end - first, b, slot, frag_row0, l);
             counts.push_back(l.size() - before);
+            frag_row0 += ((end - first) * tokens_ + 31) / 32 * 32;
         }
         check(dhx_record_branches(engine_.get(), key(b, slot), l.data(), counts.data(), nb), engine_.get());
     }
 
     // The launches for images [first, first + n) of a batch of b.
-    void plan(uint64_t first, uint64_t n, uint64_t b, uint32_t slot, std::vector<dhx_launch>& l) const {
+    void plan(uint64_t first, uint64_t n, uint64_t b, uint32_t slot, uint64_t frag_row0,
+              std::vector<dhx_launch>& l) const {
         const uint32_t r = (uint32_t)(n * tokens_);
         const uint32_t B = (uint32_t)n, G = grid_, TP = (uint32_t)tpad_;
         auto add = [&](uint32_t kernel, std::initializer_list<uint32_t> s, std::initializer_list<dhx_region> bind) {
@@ -254,11 +260,18 @@ public:
             g.bytes = n * per_image;
             return g;
         };
+        // This group's rows of a fragment-order activation buffer of width k.
+        auto frag_part = [&](int buf, uint64_t k) {
+            dhx_region g = a_[buf];
+            g.offset += frag_row0 * k * 2;
+            g.bytes = (n * tokens_ + 31) / 32 * 32 * k * 2;
+            return g;
+        };
         const uint64_t row = tokens_ * kHiddenU;
         const uint64_t heads = 6 * tpad_ * 64 * 2;
-        const dhx_region X = part(kX, row * 2), H = part(kH, row * 2), S = part(kStats, tokens_ * 12 * 4);
+        const dhx_region X = frag_part(kX, kHiddenU), H = frag_part(kH, kHiddenU), S = part(kStats, tokens_ * 12 * 4);
         const dhx_region Q = part(kQ, heads), K = part(kK, heads), V = part(kV, heads);
-        const dhx_region A = part(kAttn, row * 2), F = part(kAct, tokens_ * 1536 * 2);
+        const dhx_region A = frag_part(kAttn, kHiddenU), F = frag_part(kAct, 1536);
         const dhx_region O = part(out_buffer(slot), row * 4), I = part(image_buffer(slot), image_elems_ * 4);
         const dhx_region SL = part(kPartials, (uint64_t)kSplits * row * 4);  // [splits][rows][384] per group
         const bool split = b == 1 || splitk_ == 1;

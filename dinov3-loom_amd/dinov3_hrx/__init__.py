@@ -120,6 +120,8 @@ def _load_library() -> ctypes.CDLL:
     L.dhx_reserve_readback.argtypes = [vp, c.c_uint64]
     L.dhx_read.argtypes = [vp, Region, vp, c.c_uint64]
     L.dhx_reserve_staging.argtypes = [vp, c.c_uint64, c.c_uint64]
+    L.dhx_fragment_order.argtypes = [vp, c.c_uint64, c.c_uint64, vp]
+    L.dhx_row_order.argtypes = [vp, c.c_uint64, c.c_uint64, vp]
     L.dhx_copy_in.argtypes = [vp, Region, vp, c.c_uint64, c.c_uint32]
     L.dhx_replay_slot.argtypes = [vp, c.c_uint64, c.c_uint32]
     L.dhx_copy_out.argtypes = [vp, Region, c.c_uint64, c.c_uint32]
@@ -320,6 +322,27 @@ def patchify(pixels, image_size: int = 224) -> np.ndarray:
     g = image_size // 16
     out = np.empty((images * g * g, 768), np.float32)
     _check(_lib.dinov3_patchify(_fptr(px), images, int(image_size), _fptr(out)))
+    return out
+
+
+def fragment_order(a: np.ndarray) -> np.ndarray:
+    """Row-major f16 [rows][k] -> the kernels' fragment order (rows padded to 32)."""
+    a = np.ascontiguousarray(a, np.float16)
+    rows, k = a.shape
+    out = np.empty(((rows + 31) // 32 * 32 * k,), np.float16)
+    if _lib.dhx_fragment_order(a.ctypes.data, rows, k, out.ctypes.data) != 0:
+        raise DINOv3Error(_lib.dhx_last_error(None).decode())
+    return out
+
+
+def row_order(f: np.ndarray, rows: int, k: int) -> np.ndarray:
+    """Inverse of fragment_order."""
+    f = np.ascontiguousarray(f, np.float16)
+    if f.size < (rows + 31) // 32 * 32 * k:
+        raise DINOv3Error("fragment buffer too small")
+    out = np.empty((rows, k), np.float16)
+    if _lib.dhx_row_order(f.ctypes.data, rows, k, out.ctypes.data) != 0:
+        raise DINOv3Error(_lib.dhx_last_error(None).decode())
     return out
 
 

@@ -57,6 +57,15 @@ typedef struct dhx_region {
  * input algebraically from those statistics: with W' = gamma (.) W (f16),
  * wsum[n] = sum_k W'[n][k] and t = b + beta . W^T, out = rstd * (x . W'^T -
  * mean * wsum) + t equals LN(x) . W^T + b.
+ * The f16 activations x (patch_embed, resid and reduce output, QKV / SwiGLU
+ * input with LayerNorm folded in), h (LayerNorm output), attn (attention
+ * output) and act (SwiGLU output) are in fragment order, rows padded to a
+ * multiple of 32: for A[rows][K], the 8 halfs of row m, columns k8 .. k8+7
+ * (k8 % 8 == 0) start at element ((m/32)*(K/16) + k8/16)*512 +
+ * ((k8/8)%2*32 + m%32)*8 — each 32-row x 16-column block is the 1 KB operand
+ * a wave feeds one v_mfma_f32_32x32x16_f16, so GEMMs load activations straight
+ * into registers. Binding sizes count the padded rows. dhx_fragment_order and
+ * dhx_row_order convert on the host.
  * q, k and v are [images][6][tpad][64] f16 (rows T .. tpad-1 are never
  * written and must hold finite values for attention: regions from
  * dhx_allocate start zeroed), tpad a multiple of 128 >= T = grid*grid + 5;
@@ -148,6 +157,14 @@ int dhx_read(dhx_engine *e, dhx_region r, void *out, uint64_t n);
 /* engine.rs:130-190 (benchmark): samples >= 10; samples + 10 iterations of
  * graph replay and direct dispatch in alternating order, first 10 dropped. */
 int dhx_benchmark(dhx_engine *e, uint64_t batch, uint64_t samples, dhx_timings *out);
+
+/* Host-side layout conversion for fragment-order activations (no GPU work,
+ * no reference counterpart): rows x k f16 values (k a multiple of 16)
+ * between row-major and fragment order; the fragment buffer holds
+ * ceil(rows/32)*32*k values (padding rows zero on the way in, dropped on the
+ * way out). */
+int dhx_fragment_order(const uint16_t *rows_in, uint64_t rows, uint64_t k, uint16_t *frag_out);
+int dhx_row_order(const uint16_t *frag_in, uint64_t rows, uint64_t k, uint16_t *rows_out);
 
 /* Pipelined transfers (no reference counterpart; the reference uploads,
  * replays and reads back one chunk at a time, lib.rs:98-112). Two slots,

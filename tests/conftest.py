@@ -70,3 +70,21 @@ def cosine(a, b) -> float:
     a = np.asarray(a, np.float64).ravel()
     b = np.asarray(b, np.float64).ravel()
     return float(a @ b / np.sqrt((a @ a) * (b @ b)))
+
+
+def to_frag(a):
+    """Row-major [rows][k] -> fragment order (rows padded to 32 with zeros):
+    32-row x 16-column blocks of 64 lanes x 8 values, lane hi*32 + l holding
+    row l, columns 8hi .. 8hi+7 of the block; blocks row-block-major."""
+    a = np.asarray(a)
+    rows, k = a.shape
+    rp = (rows + 31) // 32 * 32
+    p = np.zeros((rp, k), a.dtype)
+    p[:rows] = a
+    return np.ascontiguousarray(p.reshape(rp // 32, 32, k // 16, 2, 8).transpose(0, 2, 3, 1, 4))
+
+
+def from_frag(f, rows, k):
+    """Inverse of to_frag (padding rows dropped)."""
+    rp = (rows + 31) // 32 * 32
+    return np.asarray(f).reshape(rp // 32, k // 16, 2, 32, 8).transpose(0, 3, 1, 2, 4).reshape(rp, k)[:rows]

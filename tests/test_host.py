@@ -157,6 +157,26 @@ def test_patchify_kat():
     assert np.array_equal(d.patchify(big, 512), oracle.patchify(big, 32))
 
 
+def test_fragment_order_layout():
+    # The kernels' activation layout (dinov3_engine.h): row m, columns
+    # k8..k8+7 at ((m/32)*(K/16) + k8/16)*512 + ((k8/8)%2*32 + m%32)*8.
+    from conftest import from_frag, to_frag
+
+    rng = np.random.default_rng(2)
+    for rows, k in [(1, 16), (33, 384), (201, 1536), (64, 32)]:
+        a = rng.normal(size=(rows, k)).astype(np.float16)
+        f = d.fragment_order(a)
+        assert np.array_equal(f, to_frag(a).reshape(-1))
+        assert np.array_equal(d.row_order(f, rows, k), a)
+        assert np.array_equal(from_frag(f, rows, k), a)
+        for m, k8 in [(0, 0), (rows - 1, k - 8), (rows // 2, (k // 2) & ~7)]:
+            o = ((m // 32) * (k // 16) + k8 // 16) * 512 + ((k8 // 8) % 2 * 32 + m % 32) * 8
+            assert np.array_equal(f[o:o + 8], a[m, k8:k8 + 8])
+    assert not d.fragment_order(np.ones((3, 16), np.float16))[3 * 8:32 * 8].any()  # padding rows zero
+    with pytest.raises(d.DINOv3Error, match="k % 16"):
+        d.fragment_order(np.ones((2, 24), np.float16))
+
+
 def test_random_weights_deterministic_and_shaped(weight_file):
     from safetensors.numpy import load_file
 

@@ -14,7 +14,7 @@ import pytest
 import dinov3_hrx as d
 import oracle
 
-from conftest import cosine
+from conftest import cosine, from_frag, to_frag
 
 pytestmark = pytest.mark.gpu
 
@@ -50,6 +50,20 @@ def f16(a):
     return np.asarray(a, np.float16)
 
 
+# The kernels keep the f16 activations (x, h, attn, act) in fragment order;
+# these move test data between that layout and row-major numpy arrays.
+def upf(e, a):
+    return up(e, to_frag(np.asarray(a)))
+
+
+def allocf(e, rows, k):
+    return e.allocate((rows + 31) // 32 * 32 * k * 2)
+
+
+def readf(e, region, rows, k):
+    return from_frag(e.read(region, np.float16, ((rows + 31) // 32 * 32 * k,)), rows, k)
+
+
 def check(gpu, ref, atol, rel=2.0**-10, cos_min=0.99999, what=""):
     g = np.asarray(gpu, np.float64)
     r = np.asarray(ref, np.float64)
@@ -73,11 +87,11 @@ def test_pipelined_transfer_slots(eng):
     with pytest.raises(d.DINOv3Error, match="staging was not reserved"):
         eng.copy_out(eng.allocate(16), 16, 0)
     rows = 2000
-    eng.reserve_staging(rows * 384 * 2, rows * 384 * 4)
+    eng.reserve_staging(2016 * 384 * 2, rows * 384 * 4)
     g = np.ones(384, np.float32)
     b = np.zeros(384, np.float32)
     G, B = up(eng, g), up(eng, b)
-    xin = [eng.allocate(rows * 384 * 2) for _ in range(2)]
+    xin = [allocf(eng, rows, 384) for _ in range(2)]
     yout = [eng.allocate(rows * 384 * 4) for _ in range(2)]
     keys = [next(_keys), next(_keys)]
     for s in range(2):
@@ -88,7 +102,7 @@ def test_pipelined_transfer_slots(eng):
     for i in range(7):
         if i < 6:
             s = i % 2
-            eng.copy_in(xin[s], xs[i], s)
+            eng.copy_in(xin[s], to_frag(xs[i]), s)
             eng.replay_slot(keys[s], s)
             eng.copy_out(yout[s], rows * 384 * 4, s)
         if i > 0:
@@ -96,7 +110,7 @@ def test_pipelined_transfer_slots(eng):
     for i in range(6):
         check(got[i], oracle.layernorm(xs[i].astype(np.float64), g, b), atol=2e-5, rel=1e-5, what=f"slot round {i}")
     with pytest.raises(d.DINOv3Error, match="staging slot must be 0 or 1"):
-        eng.copy_in(xin[0], xs[0], 2)
+        eng.copy_in(xin[0], to_frag(xs[0]), 2)
     with pytest.raises(d.DINOv3Error, match="exceeds reserved staging"):
         eng.copy_out(eng.allocate(rows * 384 * 8), rows * 384 * 8, 0)
 
@@ -120,8 +134,8 @@ def test_record_branches(eng):
     g = rng.normal(size=384).astype(np.float32)
     b = rng.normal(size=384).astype(np.float32)
     G, B = up(eng, g), up(eng, b)
-    ins = [up(eng, x) for x in xs]
-    mid = [eng.allocate(3000 * 384 * 2) for _ in xs]
+    ins = [upf(eng, x) for x in xs]
+    mid = [allocf(eng, 3000, 384) for _ in xs]
     outs = [eng.allocate(3000 * 384 * 4) for _ in xs]
     branches = [[(K_LN, [3000], [ins[i], G, B, mid[i]]), (K_LN32, [3000], [mid[i], G, B, outs[i]])] for i in range(3)]
     key = next(_keys)
@@ -150,18 +164,18 @@ def test_layernorm(eng, rows, f32_out):
     x[0] = 1.5  # a constant row normalises to beta
     g = rng.normal(size=384).astype(np.float32)
     b = rng.normal(size=384).astype(np.float32)
-    out = eng.allocate(rows * 384 * (4 if f32_out else 2))
-    run(eng, K_LN32 if f32_out else K_LN, [rows], [up(eng, x), up(eng, g), up(eng, b), out])
-    y = eng.read(out, np.float32 if f32_out else np.float16, (rows, 384))
+    out = eng.allocate(rows * 384 * 4) if f32_out else allocf(eng, rows, 384)
+    run(eng, K_LN32 if f32_out else K_LN, [rows], [upf(eng, x), up(eng, g), up(eng, b), out])
+    y = eng.read(out, np.float32, (rows, 384)) if f32_out else readf(eng, out, rows, 384)
     ref = oracle.layernorm(x.astype(np.float64), g, b)
     check(y, ref, atol=1e-4 if not f32_out else 2e-5, rel=2.0**-10 if not f32_out else 1e-5, what=f"LN rows={rows}")
 
 
 def patch_case(eng, images, grid, px, w, b, prefix):
     T = grid * grid + 5
-    x = eng.allocate(images * T * 384 * 2)
+    x = allocf(eng, images * T, 384)
     run(eng, K_PATCH, [images, grid], [up(eng, px), up(eng, w), up(eng, b), up(eng, prefix), x])
-    return eng.read(x, np.float16, (images, T, 384))
+    return readf(eng, x, images * T, 384).reshape(images, T, 384)
 
 
 @pytest.mark.parametrize("images,grid", [(3, 14), (1, 32), (5, 4)])
@@ -217,7 +231,7 @@ def test_qkv_rope(eng, images, grid):
     sin[:, 32:] = np.nan
     nb = images * 6 * tpad * 64 * 2
     q, k, v = eng.allocate(nb), eng.allocate(nb), eng.allocate(nb)
-    run(eng, K_QKV, [images, grid, tpad], [up(eng, h), up(eng, w), up(eng, b), up(eng, cos), up(eng, sin), q, k, v])
+    run(eng, K_QKV, [images, grid, tpad], [upf(eng, h), up(eng, w), up(eng, b), up(eng, cos), up(eng, sin), q, k, v])
     gq = eng.read(q, np.float16, (images, 6, tpad, 64))
     gk = eng.read(k, np.float16, (images, 6, tpad, 64))
     gv = eng.read(v, np.float16, (images, 6, tpad, 64))
@@ -243,11 +257,11 @@ def test_attention(eng, images, grid, qscale):
     q = f16(rng.normal(size=(images * T, 384)) * qscale)
     k = f16(rng.normal(size=(images * T, 384)))
     v = f16(rng.normal(size=(images * T, 384)))
-    out = eng.allocate(images * T * 384 * 2)
+    out = allocf(eng, images * T, 384)
     run(eng, K_ATTN, [images, grid, tpad],
         [up(eng, head_major(q, images, T, tpad)), up(eng, head_major(k, images, T, tpad)),
          up(eng, head_major(v, images, T, tpad)), out])
-    y = eng.read(out, np.float16, (images * T, 384))
+    y = readf(eng, out, images * T, 384)
     for i in range(images):
         sl = slice(i * T, (i + 1) * T)
         ref = oracle.attention(q[sl].astype(np.float64), k[sl].astype(np.float64), v[sl].astype(np.float64))
@@ -262,9 +276,9 @@ def test_resid(eng, rows, kdim):
     b = (rng.normal(size=384) * 0.1).astype(np.float32)
     ls = rng.uniform(0.5, 1.5, size=384).astype(np.float32)
     x0 = f16(rng.normal(size=(rows, 384)))
-    x = up(eng, x0)
-    run(eng, K_RESID, [rows, kdim], [up(eng, a), up(eng, w), up(eng, b), up(eng, ls), x])
-    y = eng.read(x, np.float16, (rows, 384))
+    x = upf(eng, x0)
+    run(eng, K_RESID, [rows, kdim], [upf(eng, a), up(eng, w), up(eng, b), up(eng, ls), x])
+    y = readf(eng, x, rows, 384)
     ref = x0.astype(np.float64) + ls * oracle.linear(a.astype(np.float64), w.astype(np.float64), b)
     check(y, ref, atol=2e-3, what=f"resid rows={rows} k={kdim}")
 
@@ -288,9 +302,9 @@ def test_swiglu(eng, rows):
     wg, wu = f16(rng.normal(size=(1536, 384)) * 0.05), f16(rng.normal(size=(1536, 384)) * 0.05)
     bg, bu = (rng.normal(size=1536) * 0.2).astype(np.float32), (rng.normal(size=1536) * 0.2).astype(np.float32)
     w, b = pack_gateup(wg, wu, bg, bu)
-    act = eng.allocate(rows * 1536 * 2)
-    run(eng, K_SWIGLU, [rows], [up(eng, h), up(eng, w), up(eng, b), act])
-    y = eng.read(act, np.float16, (rows, 1536))
+    act = allocf(eng, rows, 1536)
+    run(eng, K_SWIGLU, [rows], [upf(eng, h), up(eng, w), up(eng, b), act])
+    y = readf(eng, act, rows, 1536)
     hd = h.astype(np.float64)
     ref = oracle.swiglu(oracle.linear(hd, wg.astype(np.float64), bg), oracle.linear(hd, wu.astype(np.float64), bu))
     check(y, ref, atol=2e-3, what=f"swiglu rows={rows}")
@@ -306,16 +320,16 @@ def test_splitk_and_reduce(eng, rows):
     ls = rng.uniform(0.5, 1.5, size=384).astype(np.float32)
     x0 = f16(rng.normal(size=(rows, 384)))
     part = eng.allocate(splits * rows * 384 * 4)
-    run(eng, K_SPLITK, [rows, kdim, splits], [up(eng, a), up(eng, w), part])
+    run(eng, K_SPLITK, [rows, kdim, splits], [upf(eng, a), up(eng, w), part])
     p = eng.read(part, np.float32, (splits, rows, 384))
     ad, wd = a.astype(np.float64), w.astype(np.float64)
     c = kdim // splits
     for s in range(splits):
         ref = oracle.linear(ad[:, s * c:(s + 1) * c], wd[:, s * c:(s + 1) * c])
         check(p[s], ref, atol=1e-4, rel=1e-5, what=f"split {s}")
-    x = up(eng, x0)
+    x = upf(eng, x0)
     run(eng, K_REDUCE, [rows, splits], [part, up(eng, b), up(eng, ls), x])
-    y = eng.read(x, np.float16, (rows, 384))
+    y = readf(eng, x, rows, 384)
     ref = x0.astype(np.float64) + ls * oracle.linear(ad, wd, b)
     check(y, ref, atol=2e-3, what="split-K reduce")
 
@@ -325,8 +339,8 @@ def test_launch_validation_happens_before_any_launch(eng):
     g = up(eng, np.ones(384, np.float32))
     with pytest.raises(d.DINOv3Error, match="needs"):
         eng.record(next(_keys), [(K_LN, [10], [small, g, g, small])])
-    big = eng.allocate(10 * 384 * 2 + 64)
-    mis = d.region_slice(big, 8, 10 * 384 * 2)
+    big = eng.allocate(32 * 384 * 2 + 64)
+    mis = d.region_slice(big, 8, 32 * 384 * 2)
     with pytest.raises(d.DINOv3Error, match="aligned"):
         eng.record(next(_keys), [(K_LN, [10], [mis, g, g, big])])
     with pytest.raises(d.DINOv3Error, match="unknown kernel"):
@@ -374,9 +388,9 @@ def test_resid_stats(eng, rows, kdim):
     b = (rng.normal(size=384) * 0.1).astype(np.float32)
     ls = rng.uniform(0.5, 1.5, size=384).astype(np.float32)
     x0 = f16(rng.normal(size=(rows, 384)) * 2 + 0.7)
-    x, st = up(eng, x0), eng.allocate(rows * 48)
-    run(eng, K_RESID_S, [rows, kdim], [up(eng, a), up(eng, w), up(eng, b), up(eng, ls), x, st])
-    y = eng.read(x, np.float16, (rows, 384))
+    x, st = upf(eng, x0), eng.allocate(rows * 48)
+    run(eng, K_RESID_S, [rows, kdim], [upf(eng, a), up(eng, w), up(eng, b), up(eng, ls), x, st])
+    y = readf(eng, x, rows, 384)
     ref = x0.astype(np.float64) + ls * oracle.linear(a.astype(np.float64), w.astype(np.float64), b)
     check(y, ref, atol=2e-3, what=f"resid+stats rows={rows} k={kdim}")
     check_stats(eng.read(st, np.float32, (rows, 12)), y, "resid stats")
@@ -389,9 +403,9 @@ def test_splitk_reduce_stats(eng, rows):
     b = (rng.normal(size=384) * 0.1).astype(np.float32)
     ls = rng.uniform(0.5, 1.5, size=384).astype(np.float32)
     x0 = f16(rng.normal(size=(rows, 384)))
-    x, st = up(eng, x0), eng.allocate(rows * 48)
+    x, st = upf(eng, x0), eng.allocate(rows * 48)
     run(eng, K_REDUCE_S, [rows, 4], [up(eng, part), up(eng, b), up(eng, ls), x, st])
-    y = eng.read(x, np.float16, (rows, 384))
+    y = readf(eng, x, rows, 384)
     ref = x0.astype(np.float64) + ls * (part.astype(np.float64).sum(0) + b)
     check(y, ref, atol=2e-3, what="reduce+stats")
     check_stats(eng.read(st, np.float32, (rows, 12)), y, "reduce stats")
@@ -406,9 +420,9 @@ def test_patch_embed_stats(eng, images, grid):
     b = (rng.normal(size=384) * 0.1).astype(np.float32)
     prefix = rng.normal(size=(5, 384)).astype(np.float32)
     pstats = slot_stats(f16(prefix))
-    x, st = eng.allocate(images * T * 768), eng.allocate(images * T * 48)
+    x, st = allocf(eng, images * T, 384), eng.allocate(images * T * 48)
     run(eng, K_PATCH_S, [images, grid], [up(eng, px), up(eng, w), up(eng, b), up(eng, prefix), up(eng, pstats), x, st])
-    y = eng.read(x, np.float16, (images, T, 384))
+    y = readf(eng, x, images * T, 384).reshape(images, T, 384)
     a = oracle.round_f16(oracle.patchify(px, grid))
     ref = oracle.linear(a, w.astype(np.float64), b).reshape(images, grid * grid, 384)
     check(y[:, 5:], ref, atol=2e-4, what="patch embed (stats variant)")
@@ -430,7 +444,7 @@ def test_qkv_rope_layernorm_fused(eng, images, grid, offset):
     nb = images * 6 * tpad * 64 * 2
     q, k, v = eng.allocate(nb), eng.allocate(nb), eng.allocate(nb)
     run(eng, K_QKV_LN, [images, grid, tpad],
-        [up(eng, x), up(eng, slot_stats(x)), up(eng, wl), up(eng, wsum), up(eng, t), up(eng, cos), up(eng, sin),
+        [upf(eng, x), up(eng, slot_stats(x)), up(eng, wl), up(eng, wsum), up(eng, t), up(eng, cos), up(eng, sin),
          q, k, v])
     gq = eng.read(q, np.float16, (images, 6, tpad, 64))
     gv = eng.read(v, np.float16, (images, 6, tpad, 64))
@@ -453,9 +467,9 @@ def test_swiglu_layernorm_fused(eng, rows, offset):
     bg, bu = (rng.normal(size=1536) * 0.2).astype(np.float32), (rng.normal(size=1536) * 0.2).astype(np.float32)
     w, b = pack_gateup(wg, wu, bg, bu)
     wl, wsum, t = fold(w, b, gamma, beta)
-    act = eng.allocate(rows * 1536 * 2)
-    run(eng, K_SWIGLU_LN, [rows], [up(eng, x), up(eng, slot_stats(x)), up(eng, wl), up(eng, wsum), up(eng, t), act])
-    y = eng.read(act, np.float16, (rows, 1536))
+    act = allocf(eng, rows, 1536)
+    run(eng, K_SWIGLU_LN, [rows], [upf(eng, x), up(eng, slot_stats(x)), up(eng, wl), up(eng, wsum), up(eng, t), act])
+    y = readf(eng, act, rows, 1536)
     h = oracle.layernorm(x.astype(np.float64), gamma, beta)
     ref = oracle.swiglu(oracle.linear(h, wg.astype(np.float64), bg), oracle.linear(h, wu.astype(np.float64), bu))
     check(y, ref, atol=3e-3, what=f"fused-LN swiglu rows={rows}")
