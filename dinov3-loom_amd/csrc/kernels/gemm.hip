@@ -14,7 +14,7 @@ using gemm::tiles_for;
 using PatchTile = Tile<64, 128, 2, 2>;
 using QkvTile = Tile<128, 128, 4, 1>;
 using ResidTile = Tile<128, 128, 4, 1>;
-using SwigluTile = Tile<128, 128, 4, 1>;
+using SwigluTile = Tile<256, 128, 4, 1, 32>;
 using SplitTile = Tile<128, 128, 4, 1>;
 
 template <class T, class Args>

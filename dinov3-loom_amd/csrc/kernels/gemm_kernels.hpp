@@ -286,11 +286,11 @@ __global__ __launch_bounds__(T::THREADS) void resid_kernel(ResidArgs p) {
 
 // SwiGLU dual GEMM. W rows are packed as blocks of 32 gate rows followed by
 // the 32 matching up rows, so a wave's 128 columns are two gate/up pairs of
-// 32 outputs each. Each wave stages its 32 x 64 block of act in LDS and
-// writes it as four whole fragments (act is in fragment order).
+// 32 outputs each. Each wave stages its TM x 64 block of act in LDS and
+// writes it as whole fragments (act is in fragment order).
 template <class T, bool LN>
-__global__ __launch_bounds__(T::THREADS, 3) void swiglu_kernel(SwigluArgs p) {
-    static_assert(T::TN % 64 == 0 && T::TM == 32 && T::WGN == 1, "whole gate/up pairs, one 32-row block per wave");
+__global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void swiglu_kernel(SwigluArgs p) {
+    static_assert(T::TN % 64 == 0 && T::WGN == 1, "whole gate/up pairs, whole rows per wave");
     constexpr int OW = T::TN / 2;  // act columns per wave
     constexpr int SP = OW + 8;     // staging pitch in halfs
     constexpr int LDS = T::WAVES * T::TM * SP > 2 * T::W_HALFS ? T::WAVES * T::TM * SP : 2 * T::W_HALFS;
@@ -303,34 +303,40 @@ __global__ __launch_bounds__(T::THREADS, 3) void swiglu_kernel(SwigluArgs p) {
                        [&](const Acc<T>& acc, int m0, int n0) {
         const Frag<T> f(m0, n0);
         half_t* const st = lds + (threadIdx.x >> 6) * T::TM * SP;
-        RowNorm rn{0.f, 1.f};
-        if constexpr (LN) rn = row_norm(p.stats, min(f.row(0), p.rows - 1));
         // Pair q of the wave: gate = acc.v[2q], up = acc.v[2q + 1], outputs
         // 32q .. 32q+31 of the wave's OW. Column constants are loaded per
         // register group to keep the register footprint small next to acc.
 #pragma unroll
-        for (int q = 0; q < T::FN / 2; ++q)
+        for (int j = 0; j < T::FM; ++j) {
+            RowNorm rn{0.f, 1.f};
+            if constexpr (LN) rn = row_norm(p.stats, min(f.row(j), p.rows - 1));
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int c = g * 8 + f.hi * 4, n = f.n_base + 64 * q + c;
-                float4_t gate = group4(acc.v[2 * q][0], g), up = group4(acc.v[2 * q + 1][0], g);
-                if constexpr (LN) {
-                    gate = (gate - rn.mean * ld4(p.wsum + n)) * rn.rstd;
-                    up = (up - rn.mean * ld4(p.wsum + n + 32)) * rn.rstd;
+            for (int q = 0; q < T::FN / 2; ++q)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int c = g * 8 + f.hi * 4, n = f.n_base + 64 * q + c;
+                    float4_t gate = group4(acc.v[2 * q][j], g), up = group4(acc.v[2 * q + 1][j], g);
+                    if constexpr (LN) {
+                        gate = (gate - rn.mean * ld4(p.wsum + n)) * rn.rstd;
+                        up = (up - rn.mean * ld4(p.wsum + n + 32)) * rn.rstd;
+                    }
+                    gate += ld4(p.bias + n);
+                    up += ld4(p.bias + n + 32);
+                    const float4_t y = float4_t{silu(gate[0]), silu(gate[1]), silu(gate[2]), silu(gate[3])} * up;
+                    *(half4_t*)(st + (j * 32 + f.l32) * SP + 32 * q + c) = to_half4(y);
                 }
-                gate += ld4(p.bias + n);
-                up += ld4(p.bias + n + 32);
-                const float4_t y = float4_t{silu(gate[0]), silu(gate[1]), silu(gate[2]), silu(gate[3])} * up;
-                *(half4_t*)(st + f.l32 * SP + 32 * q + c) = to_half4(y);
-            }
+        }
         wave_lds_sync();
-        const int mb = f.m_base / 32;
-        if (mb >= (p.rows + 31) / 32) return;  // uniform per wave
-        const int lane = threadIdx.x & 63;
+        const int lane = threadIdx.x & 63, mblocks = (p.rows + 31) / 32;
 #pragma unroll
-        for (int ks = 0; ks < OW / 16; ++ks)
-            *(half8_t*)(p.act + ((size_t)mb * (kFF / 16) + f.n_base / 32 + ks) * 512 + lane * 8) =
-                *(const half8_t*)(st + f.l32 * SP + ks * 16 + f.hi * 8);
+        for (int j = 0; j < T::FM; ++j) {
+            const int mb = f.m_base / 32 + j;
+            if (mb >= mblocks) break;  // uniform per wave
+#pragma unroll
+            for (int ks = 0; ks < OW / 16; ++ks)
+                *(half8_t*)(p.act + ((size_t)mb * (kFF / 16) + f.n_base / 32 + ks) * 512 + lane * 8) =
+                    *(const half8_t*)(st + (j * 32 + f.l32) * SP + ks * 16 + f.hi * 8);
+        }
     });
 }
 
