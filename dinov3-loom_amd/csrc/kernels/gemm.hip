@@ -10,10 +10,12 @@ using gemm::tiles_for;
 
 // The patch embedding stages both operands in LDS (its A operand is gathered
 // from pixels); the others take activations in fragment order straight into
-// registers, four waves stacked along M.
+// registers, waves stacked along M. The residual GEMMs (N = 384: too few
+// 128x128 tiles to fill 256 CUs) use 128x64 tiles, twice as many workgroups
+// of a quarter of the registers.
 using PatchTile = Tile<64, 128, 2, 2>;
 using QkvTile = Tile<128, 128, 4, 1>;
-using ResidTile = Tile<128, 128, 4, 1>;
+using ResidTile = Tile<128, 64, 4, 1>;
 using SwigluTile = Tile<256, 128, 4, 1, 32>;
 using SplitTile = Tile<128, 128, 4, 1>;
 
@@ -38,6 +40,8 @@ hipError_t launch_qkv_rope(const QkvArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_resid(const ResidArgs& a, hipStream_t s) {
+    // The K loop walks its stages two at a time.
+    if (a.k % (2 * ResidTile::BK) != 0) return hipErrorInvalidValue;
     const int tiles = tiles_for<ResidTile>(a.rows, kHidden);
     return a.stats ? launch<ResidTile>(gemm::resid_kernel<ResidTile, true>, tiles, a, s)
                    : launch<ResidTile>(gemm::resid_kernel<ResidTile, false>, tiles, a, s);

@@ -147,8 +147,8 @@ __device__ __forceinline__ void init_frags(ActFrags<T> (&al)[2], const half_t* a
 // q, k and v are all head-major [image][head][tpad][64], and the rows of one
 // image are contiguous there.
 template <class T, bool LN>
-__global__ __launch_bounds__(T::THREADS, 3) void qkv_rope_kernel(QkvArgs p) {
-    static_assert(T::TN == 2 * kHeadDim && T::TM == 32, "two heads per wave");
+__global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void qkv_rope_kernel(QkvArgs p) {
+    static_assert(T::TN == 2 * kHeadDim && T::WGN == 1, "two heads per wave, whole rows per wave");
     constexpr int SP = T::TN + 8;  // staging pitch in halfs
     constexpr int LDS = T::WAVES * T::TM * SP > 2 * T::W_HALFS ? T::WAVES * T::TM * SP : 2 * T::W_HALFS;
     __shared__ __attribute__((aligned(16))) half_t lds[LDS];
@@ -162,48 +162,52 @@ __global__ __launch_bounds__(T::THREADS, 3) void qkv_rope_kernel(QkvArgs p) {
         const int lane = threadIdx.x & 63;
         half_t* const st = lds + (threadIdx.x >> 6) * (T::TM * SP);
         const int part = f.n_base / kHidden, head0 = (f.n_base % kHidden) / kHeadDim;
-        const int m = min(f.m_base + f.l32, M - 1);  // rows past M are computed but never written out
-        const int tok = m % Tok;
-        // RoPE angles of this row, gathered together before any use (lanes
-        // hold different rows); prefix rows and v rotate by cos 1, sin 0.
-        const size_t angle_row = (size_t)max(tok - kPrefix, 0) * kHeadDim;
-        float4_t co[4], si[4];
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            co[g] = float4_t{1.f, 1.f, 1.f, 1.f};
-            si[g] = float4_t{};
-            if (part < 2) {  // uniform per wave
-                co[g] = ld4(p.cos + angle_row + g * 8 + f.hi * 4);
-                si[g] = ld4(p.sin + angle_row + g * 8 + f.hi * 4);
-            }
-        }
-        if (tok < kPrefix) {
+        for (int j = 0; j < T::FM; ++j) {
+            const int m = min(f.row(j), M - 1);  // rows past M are computed but never written out
+            const int tok = m % Tok;
+            // RoPE angles of this row, gathered together before any use (lanes
+            // hold different rows); prefix rows and v rotate by cos 1, sin 0.
+            const size_t angle_row = (size_t)max(tok - kPrefix, 0) * kHeadDim;
+            float4_t co[4], si[4];
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 co[g] = float4_t{1.f, 1.f, 1.f, 1.f};
                 si[g] = float4_t{};
-            }
-        }
-        RowNorm rn{0.f, 1.f};
-        if constexpr (LN) rn = row_norm(p.stats, m);
-#pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int c = g * 8 + f.hi * 4;  // channel in the head (0..31); partner c + 32
-                const int n = f.n_base + h2 * kHeadDim + c;
-                float4_t lo = group4(acc.v[2 * h2][0], g), up = group4(acc.v[2 * h2 + 1][0], g);
-                if constexpr (LN) {
-                    lo = (lo - rn.mean * ld4(p.wsum + n)) * rn.rstd;
-                    up = (up - rn.mean * ld4(p.wsum + n + 32)) * rn.rstd;
+                if (part < 2) {  // uniform per wave
+                    co[g] = ld4(p.cos + angle_row + g * 8 + f.hi * 4);
+                    si[g] = ld4(p.sin + angle_row + g * 8 + f.hi * 4);
                 }
-                lo += ld4(p.bias + n);
-                up += ld4(p.bias + n + 32);
-                const float4_t nlo = lo * co[g] - up * si[g];  // x[c] cos - x[c+32] sin
-                const float4_t nup = up * co[g] + lo * si[g];  // x[c+32] cos + x[c] sin
-                *(half4_t*)(st + f.l32 * SP + h2 * kHeadDim + c) = to_half4(nlo);
-                *(half4_t*)(st + f.l32 * SP + h2 * kHeadDim + 32 + c) = to_half4(nup);
             }
+            if (tok < kPrefix) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    co[g] = float4_t{1.f, 1.f, 1.f, 1.f};
+                    si[g] = float4_t{};
+                }
+            }
+            RowNorm rn{0.f, 1.f};
+            if constexpr (LN) rn = row_norm(p.stats, m);
+            half_t* const srow = st + (j * 32 + f.l32) * SP;
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int c = g * 8 + f.hi * 4;  // channel in the head (0..31); partner c + 32
+                    const int n = f.n_base + h2 * kHeadDim + c;
+                    float4_t lo = group4(acc.v[2 * h2][j], g), up = group4(acc.v[2 * h2 + 1][j], g);
+                    if constexpr (LN) {
+                        lo = (lo - rn.mean * ld4(p.wsum + n)) * rn.rstd;
+                        up = (up - rn.mean * ld4(p.wsum + n + 32)) * rn.rstd;
+                    }
+                    lo += ld4(p.bias + n);
+                    up += ld4(p.bias + n + 32);
+                    const float4_t nlo = lo * co[g] - up * si[g];  // x[c] cos - x[c+32] sin
+                    const float4_t nup = up * co[g] + lo * si[g];  // x[c+32] cos + x[c] sin
+                    *(half4_t*)(srow + h2 * kHeadDim + c) = to_half4(nlo);
+                    *(half4_t*)(srow + h2 * kHeadDim + 32 + c) = to_half4(nup);
+                }
+        }
         wave_lds_sync();
         // Copy-out: 8 lanes per 128-byte head row, 8 rows per pass.
         half_t* const out = part == 0 ? p.q : part == 1 ? p.k : p.v;
@@ -230,11 +234,11 @@ __global__ __launch_bounds__(T::THREADS, 3) void qkv_rope_kernel(QkvArgs p) {
 
 // Residual GEMM: x += ls * (A W^T + b), in place on the f16 residual stream
 // in fragment order (with STATS, also the LayerNorm row statistics of the
-// updated x). Each wave stages its f32 update (32 x 128) in LDS, then reads
+// updated x). Each wave stages its f32 update (32 x TN) in LDS, then reads
 // and writes x fragment by fragment (1 KB contiguous per wave access).
 template <class T, bool STATS>
-__global__ __launch_bounds__(T::THREADS) void resid_kernel(ResidArgs p) {
-    static_assert(T::TN == 128 && T::TM == 32, "two statistics slots per wave");
+__global__ __launch_bounds__(T::THREADS, 4) void resid_kernel(ResidArgs p) {
+    static_assert(T::TN % 64 == 0 && T::TM == 32, "whole statistics slots, one 32-row block per wave");
     constexpr int SPF = T::TN + 4;  // staging pitch in floats
     constexpr int LDS = T::WAVES * T::TM * SPF * 2 > 2 * T::W_HALFS ? T::WAVES * T::TM * SPF * 2 : 2 * T::W_HALFS;
     __shared__ __attribute__((aligned(16))) half_t lds[LDS];
@@ -261,7 +265,7 @@ __global__ __launch_bounds__(T::THREADS) void resid_kernel(ResidArgs p) {
         const bool valid = m < p.rows;
         const int lane = threadIdx.x & 63;
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
+        for (int s2 = 0; s2 < T::TN / 64; ++s2) {
             float v[32];
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) {
