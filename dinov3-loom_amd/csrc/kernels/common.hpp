@@ -86,9 +86,8 @@ struct RowNorm {
     float mean, rstd;
 };
 
-__device__ __forceinline__ RowNorm row_norm(const float* stats, size_t row) {
-    const float4_t* p = (const float4_t*)(stats + row * 12);
-    const float4_t a = p[0], b = p[1], c = p[2];
+// From a row's 12 statistics floats, loaded as three float4 (a, b, c).
+__device__ __forceinline__ RowNorm row_norm(float4_t a, float4_t b, float4_t c) {
     const float mk[6] = {a[0], a[2], b[0], b[2], c[0], c[2]};
     const float m2 = (a[1] + a[3]) + (b[1] + b[3]) + (c[1] + c[3]);
     const float mean = (((mk[0] + mk[1]) + (mk[2] + mk[3])) + (mk[4] + mk[5])) * (1.0f / 6.0f);
@@ -97,6 +96,11 @@ __device__ __forceinline__ RowNorm row_norm(const float* stats, size_t row) {
     for (int i = 0; i < 6; ++i) dev += (mk[i] - mean) * (mk[i] - mean);
     const float var = (m2 + 64.0f * dev) * (1.0f / kHidden);
     return RowNorm{mean, rsqrtf(var + 1e-5f)};
+}
+
+__device__ __forceinline__ RowNorm row_norm(const float* stats, size_t row) {
+    const float4_t* p = (const float4_t*)(stats + row * 12);
+    return row_norm(p[0], p[1], p[2]);
 }
 
 }  // namespace dhx

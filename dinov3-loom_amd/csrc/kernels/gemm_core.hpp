@@ -218,10 +218,13 @@ __device__ __forceinline__ int xcd_tile(int total) {
 // previous barrier). P = 3 gives each load two steps of latency cover for 32
 // more VGPRs. Loads past the last stage repeat it (unconditional loads keep
 // the compiler's vmcnt waits exact). The loaders take the tile origin
-// (m0, n0) and the stage.
-template <class T, int P, class AL, class WL>
+// (m0, n0) and the stage. settle() runs once the first stages' loads are
+// issued and before the first barrier: it can consume loads the caller
+// issued earlier (they are older, so waiting for them does not wait for the
+// stage loads) and write LDS that the epilogue reads.
+template <class T, int P, class AL, class WL, class Settle>
 __device__ __forceinline__ void gemm_main(AL (&al)[P], WL (&wl)[P], int m0, int n0, int k_tiles, half_t* lds,
-                                          Acc<T>& acc) {
+                                          Acc<T>& acc, Settle&& settle) {
     static_assert(P == 2 || P == 3, "register sets");
     constexpr int L = P == 2 ? 2 : 6;  // steps per unrolled block: s%2 and s%P are compile-time
     const int tid = threadIdx.x;
@@ -241,6 +244,7 @@ __device__ __forceinline__ void gemm_main(AL (&al)[P], WL (&wl)[P], int m0, int 
         wl[0].load(m0, n0, 0, tid);
         al[1].load(m0, n0, min(1, last), tid);
         wl[1].load(m0, n0, min(1, last), tid);
+        settle();
         wl[0].store(s0, tid);
         lds_barrier();
         for (int kt = 0; kt < k_tiles; kt += 2) {
@@ -261,6 +265,7 @@ __device__ __forceinline__ void gemm_main(AL (&al)[P], WL (&wl)[P], int m0, int 
             al[i].load(m0, n0, min(i, last), tid);
             wl[i].load(m0, n0, min(i, last), tid);
         }
+        settle();
         al[0].store(lds, tid);
         wl[0].store(lds + T::BM * T::LDK, tid);
         lds_barrier();
@@ -284,16 +289,29 @@ __device__ __forceinline__ void gemm_main(AL (&al)[P], WL (&wl)[P], int m0, int 
     }
 }
 
-// Runs the tile of this workgroup (if any) and its epilogue epi(acc, m0, n0).
-template <class T, int P, class AL, class WL, class Epi>
+// Runs the tile of this workgroup (if any): issue(m0, n0) first (the
+// epilogue's own loads: row statistics, column constants), then the K loop
+// with settle() after its first loads (see gemm_main), then epi(acc, m0, n0).
+// Issuing the epilogue's loads ahead of the K loop hides their latency, and
+// since they are the oldest loads, the waits that consume them do not wait
+// for the stage loads.
+template <class T, int P, class AL, class WL, class Issue, class Settle, class Epi>
 __device__ __forceinline__ void gemm_tile(AL (&al)[P], WL (&wl)[P], int n_tiles, int total_tiles, int k_tiles,
-                                          half_t* lds, Epi&& epi) {
+                                          half_t* lds, Issue&& issue, Settle&& settle, Epi&& epi) {
     const int t = xcd_tile(total_tiles);
     if (t < 0) return;  // uniform per workgroup
     const int n0 = (t % n_tiles) * T::BN, m0 = (t / n_tiles) * T::BM;
+    issue(m0, n0);
     Acc<T> acc;
-    gemm_main<T, P>(al, wl, m0, n0, k_tiles, lds, acc);
+    gemm_main<T, P>(al, wl, m0, n0, k_tiles, lds, acc, settle);
     epi(acc, m0, n0);
+}
+
+// gemm_tile without epilogue loads of its own.
+template <class T, int P, class AL, class WL, class Epi>
+__device__ __forceinline__ void gemm_tile(AL (&al)[P], WL (&wl)[P], int n_tiles, int total_tiles, int k_tiles,
+                                          half_t* lds, Epi&& epi) {
+    gemm_tile<T, P>(al, wl, n_tiles, total_tiles, k_tiles, lds, [](int, int) {}, [] {}, epi);
 }
 
 // Workgroups for a launch: one per tile (a persistent walk over several

@@ -290,42 +290,72 @@ __global__ __launch_bounds__(T::THREADS, 4) void resid_kernel(ResidArgs p) {
 
 // SwiGLU dual GEMM. W rows are packed as blocks of 32 gate rows followed by
 // the 32 matching up rows, so a wave's 128 columns are two gate/up pairs of
-// 32 outputs each. Each wave stages its TM x 64 block of act in LDS and
-// writes it as whole fragments (act is in fragment order).
+// 32 outputs each. The tile's column constants (bias, and wsum with the
+// folded LayerNorm) and its rows' statistics are loaded before the K loop;
+// the constants wait in LDS. Each wave stages its TM x 64 block of act in
+// LDS and writes it as whole fragments (act is in fragment order).
 template <class T, bool LN>
 __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void swiglu_kernel(SwigluArgs p) {
     static_assert(T::TN % 64 == 0 && T::WGN == 1, "whole gate/up pairs, whole rows per wave");
+    static_assert(T::BN <= T::THREADS, "one thread per column constant");
     constexpr int OW = T::TN / 2;  // act columns per wave
     constexpr int SP = OW + 8;     // staging pitch in halfs
     constexpr int LDS = T::WAVES * T::TM * SP > 2 * T::W_HALFS ? T::WAVES * T::TM * SP : 2 * T::W_HALFS;
     __shared__ __attribute__((aligned(16))) half_t lds[LDS];
+    __shared__ __attribute__((aligned(16))) float cst[2][T::BN];  // bias, wsum
     constexpr int NT = 2 * kFF / T::BN;
+    const int tid = threadIdx.x;
     ActFrags<T> al[2];
     init_frags(al, p.h, p.rows, kHidden);
     WeightRows<T> wl[2] = {{{}, p.w, kHidden, 0}, {{}, p.w, kHidden, 0}};
-    gemm_tile<T>(al, wl, NT, NT * ((p.rows + T::BM - 1) / T::BM), kHidden / T::BK, lds,
-                       [&](const Acc<T>& acc, int m0, int n0) {
+    float4_t raw[T::FM][3];
+    RowNorm rn[T::FM];
+    float cb = 0.f, cw = 0.f;
+    gemm_tile<T>(
+        al, wl, NT, NT * ((p.rows + T::BM - 1) / T::BM), kHidden / T::BK, lds,
+        [&](int m0, int n0) {
+            const Frag<T> f(m0, n0);
+            if constexpr (LN) {
+#pragma unroll
+                for (int j = 0; j < T::FM; ++j) {
+                    const float4_t* sp = (const float4_t*)(p.stats + (size_t)min(f.row(j), p.rows - 1) * kStatFloats);
+                    raw[j][0] = sp[0];
+                    raw[j][1] = sp[1];
+                    raw[j][2] = sp[2];
+                }
+            }
+            if (tid < T::BN) {
+                cb = p.bias[n0 + tid];
+                if constexpr (LN) cw = p.wsum[n0 + tid];
+            }
+        },
+        [&] {
+            if (tid < T::BN) {
+                cst[0][tid] = cb;
+                cst[1][tid] = cw;
+            }
+#pragma unroll
+            for (int j = 0; j < T::FM; ++j) rn[j] = LN ? row_norm(raw[j][0], raw[j][1], raw[j][2]) : RowNorm{0.f, 1.f};
+        },
+        [&](const Acc<T>& acc, int m0, int n0) {
         const Frag<T> f(m0, n0);
         half_t* const st = lds + (threadIdx.x >> 6) * T::TM * SP;
         // Pair q of the wave: gate = acc.v[2q], up = acc.v[2q + 1], outputs
-        // 32q .. 32q+31 of the wave's OW. Column constants are loaded per
-        // register group to keep the register footprint small next to acc.
+        // 32q .. 32q+31 of the wave's OW.
 #pragma unroll
         for (int j = 0; j < T::FM; ++j) {
-            RowNorm rn{0.f, 1.f};
-            if constexpr (LN) rn = row_norm(p.stats, min(f.row(j), p.rows - 1));
 #pragma unroll
             for (int q = 0; q < T::FN / 2; ++q)
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
-                    const int c = g * 8 + f.hi * 4, n = f.n_base + 64 * q + c;
+                    const int c = g * 8 + f.hi * 4, nl = f.n_base - n0 + 64 * q + c;
                     float4_t gate = group4(acc.v[2 * q][j], g), up = group4(acc.v[2 * q + 1][j], g);
                     if constexpr (LN) {
-                        gate = (gate - rn.mean * ld4(p.wsum + n)) * rn.rstd;
-                        up = (up - rn.mean * ld4(p.wsum + n + 32)) * rn.rstd;
+                        gate = (gate - rn[j].mean * *(const float4_t*)&cst[1][nl]) * rn[j].rstd;
+                        up = (up - rn[j].mean * *(const float4_t*)&cst[1][nl + 32]) * rn[j].rstd;
                     }
-                    gate += ld4(p.bias + n);
-                    up += ld4(p.bias + n + 32);
+                    gate += *(const float4_t*)&cst[0][nl];
+                    up += *(const float4_t*)&cst[0][nl + 32];
                     const float4_t y = float4_t{silu(gate[0]), silu(gate[1]), silu(gate[2]), silu(gate[3])} * up;
                     *(half4_t*)(st + (j * 32 + f.l32) * SP + 32 * q + c) = to_half4(y);
                 }
