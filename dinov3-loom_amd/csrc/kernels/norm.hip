@@ -18,9 +18,13 @@ constexpr int kLnKs = kKs / kWaves;     // blocks per wave in the LayerNorm
 // combined with the partner lane l ^ 32 and then across the four waves
 // through LDS (the reference uses E[x^2] - E[x]^2,
 // layernorm_rowwave_f16.loom:86-93); eps 1e-5. The f16 output (h) is written
-// in fragment order, the f32 output (the final tokens) row-major.
+// in fragment order; the f32 output (the final tokens, row-major) goes
+// through LDS so that each wave writes 384-byte row runs.
+constexpr int kOutPitch = kLnKs * 16 + 4;  // floats per staged row of a wave
+
 __global__ __launch_bounds__(kThreads) void layernorm_kernel(LayerNormArgs p) {
     __shared__ float part[2][kWaves][32];
+    __shared__ __attribute__((aligned(16))) float stage[kWaves][32 * kOutPitch];
     const int lane = threadIdx.x & 63, l32 = lane & 31, hi = lane >> 5, w = threadIdx.x >> 6;
     const int mb = blockIdx.x, row = mb * 32 + l32, ks0 = w * kLnKs;
     const half_t* xb = p.x + ((size_t)mb * kKs + ks0) * 512 + lane * 8;
@@ -47,7 +51,7 @@ __global__ __launch_bounds__(kThreads) void layernorm_kernel(LayerNormArgs p) {
     __syncthreads();
     d = (part[1][0][l32] + part[1][1][l32]) + (part[1][2][l32] + part[1][3][l32]);
     const float rstd = rsqrtf(d / kHidden + 1e-5f);
-    if (row >= p.rows) return;
+    float* const st = stage[w];
 #pragma unroll
     for (int i = 0; i < kLnKs; ++i) {
         const int ks = ks0 + i, c = ks * 16 + hi * 8;
@@ -60,15 +64,25 @@ __global__ __launch_bounds__(kThreads) void layernorm_kernel(LayerNormArgs p) {
             y[e + 4] = ((float)v[i][e + 4] - mean) * rstd * g1[e] + b1[e];
         }
         if (p.f32_out) {
-            float* o = (float*)p.out + (size_t)row * kHidden + c;
+            float* const o = st + l32 * kOutPitch + i * 16 + hi * 8;
             *(float4_t*)o = float4_t{y[0], y[1], y[2], y[3]};
             *(float4_t*)(o + 4) = float4_t{y[4], y[5], y[6], y[7]};
-        } else {
+        } else if (row < p.rows) {
             half8_t h;
 #pragma unroll
             for (int e = 0; e < 8; ++e) h[e] = (half_t)y[e];
             *(half8_t*)((half_t*)p.out + ((size_t)mb * kKs + ks) * 512 + lane * 8) = h;
         }
+    }
+    if (!p.f32_out) return;
+    wave_lds_sync();
+    // The wave's 32 rows x 96 columns: 24 float4 per row, 12 per lane.
+    constexpr int Q = kLnKs * 4;  // float4 per row
+#pragma unroll
+    for (int it = 0; it < 32 * Q / 64; ++it) {
+        const int idx = it * 64 + lane, r = idx / Q, q = idx % Q, m = mb * 32 + r;
+        if (m < p.rows)
+            *(float4_t*)((float*)p.out + (size_t)m * kHidden + ks0 * 16 + q * 4) = *(const float4_t*)(st + r * kOutPitch + q * 4);
     }
 }
 
