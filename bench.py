@@ -112,6 +112,32 @@ def cpu_baseline(path, seconds):
                           "sample": f"{nm} image(s), {cores} threads, {dtm:.1f} s"}}
 
 
+def library_gemms(batch, iters=50, reps=5):
+    """Vendor-library (torch.matmul -> hipBLASLt) f16 GEMMs at the forward's four shapes, for
+    comparison with the fused kernels (which also do LayerNorm folding, RoPE, SwiGLU or the
+    residual update in their epilogues). Prints a markdown table; not the metric."""
+    import torch
+    rows = batch * 201
+    print(f"| GEMM (M = {rows}) | N | K | library us | library TFLOP/s |")
+    print("|---|---|---|---|---|")
+    for name, n, k in [("gate/up", 3072, 384), ("qkv", 1152, 384), ("down", 384, 1536), ("o-proj", 384, 384)]:
+        a = torch.randn(rows, k, device="cuda", dtype=torch.float16)
+        w = torch.randn(n, k, device="cuda", dtype=torch.float16)
+        for _ in range(10):
+            a @ w.t()
+        torch.cuda.synchronize()
+        best = float("inf")
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(iters):
+                a @ w.t()
+            e1.record()
+            torch.cuda.synchronize()
+            best = min(best, e0.elapsed_time(e1) * 1e3 / iters)
+        print(f"| {name} | {n} | {k} | {best:.2f} | {2 * rows * n * k / best / 1e6:.0f} |", flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -122,10 +148,15 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--branches", type=int, default=0,
                     help="image groups run as concurrent graph branches (0: pick 1-4 by a short trial)")
+    ap.add_argument("--library-gemms", action="store_true",
+                    help="only time the vendor library's GEMMs at the forward's shapes (a reference table)")
     args = ap.parse_args()
+    if args.library_gemms:
+        library_gemms(args.batch)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (images shard across GPUs with no "
-              "exchange; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU path (the forward would shard by image, "
+              "with no exchange between GPUs). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import dinov3_hrx as d

@@ -268,7 +268,7 @@ def test_attention(eng, images, grid, qscale):
         check(y[sl], ref, atol=2.0**-9 * np.abs(v[sl]).max(), cos_min=0.9999, what=f"attention T={T} img {i}")
 
 
-@pytest.mark.parametrize("rows,kdim", [(1001, 384), (1001, 1536), (201, 1536), (12864, 384)])
+@pytest.mark.parametrize("rows,kdim", [(1, 384), (33, 1536), (1001, 384), (1001, 1536), (201, 1536), (12864, 384)])
 def test_resid(eng, rows, kdim):
     rng = np.random.default_rng(rows + kdim)
     a = f16(rng.normal(size=(rows, kdim)))
@@ -295,7 +295,7 @@ def pack_gateup(wg, wu, bg, bu):
     return w, b
 
 
-@pytest.mark.parametrize("rows", [1001, 12864])
+@pytest.mark.parametrize("rows", [1, 33, 257, 1001, 12864])
 def test_swiglu(eng, rows):
     rng = np.random.default_rng(rows)
     h = f16(rng.normal(size=(rows, 384)))
@@ -457,7 +457,7 @@ def test_qkv_rope_layernorm_fused(eng, images, grid, offset):
         check(gv[i, :, :T].transpose(1, 0, 2).reshape(T, 384), rv, atol=3e-3, what=f"fused-LN v img {i}")
 
 
-@pytest.mark.parametrize("rows,offset", [(1001, 0.0), (12864, 2.0)])
+@pytest.mark.parametrize("rows,offset", [(33, 1.0), (1001, 0.0), (12864, 2.0)])
 def test_swiglu_layernorm_fused(eng, rows, offset):
     rng = np.random.default_rng(rows + 17)
     x = f16(rng.normal(size=(rows, 384)) + offset)
