@@ -43,16 +43,10 @@ struct Tile {
     static constexpr int LDS_BYTES = LDS_HALFS * 2;
 };
 
-__device__ __forceinline__ half8_t zero8() {
-    half8_t z = {};
-    return z;
-}
-
-// Rows r0 .. r0+ROWS-1 of a row-major f16 [*][ld] matrix, 64 columns at
-// k_off + kt*64. Rows at or past `limit` re-load row limit-1: they only feed
-// output rows that are never stored, and an unconditional load keeps the
-// compiler's vmcnt accounting exact (a predicated load makes every later wait
-// drain the prefetches too).
+// Rows r0 .. r0+ROWS-1 of a row-major f16 [*][ld] matrix, BK columns from
+// k0, staged through registers into LDS rows of pitch LDK. Every load is
+// unconditional, which keeps the compiler's vmcnt accounting exact (a
+// predicated load makes every later wait drain the prefetches too).
 template <int ROWS, int THREADS, int BK, int LDK>
 struct HalfTile {
     // 16-byte chunks of one stage; when they do not split evenly over the
@@ -65,14 +59,6 @@ struct HalfTile {
     __device__ __forceinline__ static int chunk(int tid, int i) {
         const int c = tid + i * THREADS;
         return TOTAL % THREADS == 0 ? c : min(c, TOTAL - 1);
-    }
-    __device__ __forceinline__ void load(const half_t* base, int ld, int r0, int limit, int k0, int tid) {
-#pragma unroll
-        for (int i = 0; i < CHUNKS; ++i) {
-            const int c = chunk(tid, i), row = c / CPR, col = (c % CPR) * 8;
-            const int m = min(r0 + row, limit - 1);
-            r[i] = *(const half8_t*)(base + (size_t)m * ld + k0 + col);
-        }
     }
     __device__ __forceinline__ void load_all(const half_t* base, int ld, int r0, int k0, int tid) {
 #pragma unroll
@@ -88,19 +74,6 @@ struct HalfTile {
             *(half8_t*)(s + row * LDK + col) = r[i];
         }
     }
-};
-
-// A operand: f16 activations [M][lda], rows m0 .. m0+BM-1, staged in LDS.
-template <class T>
-struct ActRows {
-    static constexpr bool kInRegs = false;
-    HalfTile<T::BM, T::THREADS, T::BK, T::LDK> t;
-    const half_t* a;
-    int lda, M, k_off;
-    __device__ __forceinline__ void load(int m0, int /*n0*/, int kt, int tid) {
-        t.load(a, lda, m0, M, k_off + kt * T::BK, tid);
-    }
-    __device__ __forceinline__ void store(half_t* s, int tid) const { t.store(s, tid); }
 };
 
 // Weight operand: rows n0 .. n0+BN-1 of W[N][ldw] (the launchers only use N
@@ -210,14 +183,13 @@ __device__ __forceinline__ int xcd_tile(int total) {
     return (g >> 3) < per && t < total ? t : -1;
 }
 
-// The pipelined K loop of one tile with P register sets (P = 2 or 3) and two
-// LDS buffers: at step s the workgroup computes stage s from LDS buffer s%2,
-// the loads of stage s+P go into register set s%P (whose stage s is already
-// in LDS), and register set (s+1)%P, loaded P-1 steps earlier, is written to
+// The pipelined K loop of one tile with P = 2 register sets and two LDS
+// buffers: at step s the workgroup computes stage s from LDS buffer s%2, the
+// loads of stage s+2 go into register set s%2 (whose stage s is already in
+// LDS), and register set (s+1)%2, loaded one step earlier, is written to
 // buffer (s+1)%2 (which held stage s-1, finished by every wave at the
-// previous barrier). P = 3 gives each load two steps of latency cover for 32
-// more VGPRs. Loads past the last stage repeat it (unconditional loads keep
-// the compiler's vmcnt waits exact). The loaders take the tile origin
+// previous barrier). Loads past the last stage repeat it (unconditional
+// loads keep the compiler's vmcnt waits exact). The loaders take the tile origin
 // (m0, n0) and the stage. settle() runs once the first stages' loads are
 // issued and before the first barrier: it can consume loads the caller
 // issued earlier (they are older, so waiting for them does not wait for the
@@ -225,8 +197,7 @@ __device__ __forceinline__ int xcd_tile(int total) {
 template <class T, int P, class AL, class WL, class Settle>
 __device__ __forceinline__ void gemm_main(AL (&al)[P], WL (&wl)[P], int m0, int n0, int k_tiles, half_t* lds,
                                           Acc<T>& acc, Settle&& settle) {
-    static_assert(P == 2 || P == 3, "register sets");
-    constexpr int L = P == 2 ? 2 : 6;  // steps per unrolled block: s%2 and s%P are compile-time
+    static_assert(P == 2, "two register sets");
     const int tid = threadIdx.x;
 #pragma unroll
     for (int i = 0; i < T::FN; ++i)
@@ -237,7 +208,6 @@ __device__ __forceinline__ void gemm_main(AL (&al)[P], WL (&wl)[P], int m0, int 
         // Activations in registers, only W through LDS: register set b of
         // both operands holds the stage computed from LDS buffer b; a set is
         // refilled (two stages ahead) once that stage's MFMAs have read it.
-        static_assert(P == 2, "two register sets");
         half_t* const s0 = lds;
         half_t* const s1 = lds + T::W_HALFS;
         al[0].load(m0, n0, 0, tid);
@@ -269,19 +239,19 @@ __device__ __forceinline__ void gemm_main(AL (&al)[P], WL (&wl)[P], int m0, int 
         al[0].store(lds, tid);
         wl[0].store(lds + T::BM * T::LDK, tid);
         lds_barrier();
-        for (int base = 0; base < k_tiles; base += L) {
+        for (int base = 0; base < k_tiles; base += 2) {
 #pragma unroll
-            for (int i = 0; i < L; ++i) {
+            for (int i = 0; i < 2; ++i) {
                 const int s = base + i;
                 if (s >= k_tiles) break;  // uniform
-                half_t* const cur = lds + (i % 2) * T::STAGE_HALFS;
-                half_t* const nxt = lds + ((i + 1) % 2) * T::STAGE_HALFS;
-                al[i % P].load(m0, n0, min(s + P, last), tid);
-                wl[i % P].load(m0, n0, min(s + P, last), tid);
+                half_t* const cur = lds + i * T::STAGE_HALFS;
+                half_t* const nxt = lds + (1 - i) * T::STAGE_HALFS;
+                al[i].load(m0, n0, min(s + 2, last), tid);
+                wl[i].load(m0, n0, min(s + 2, last), tid);
                 mma_stage<T>(cur, tid, acc);
                 if (s + 1 < k_tiles) {
-                    al[(i + 1) % P].store(nxt, tid);
-                    wl[(i + 1) % P].store(nxt + T::BM * T::LDK, tid);
+                    al[1 - i].store(nxt, tid);
+                    wl[1 - i].store(nxt + T::BM * T::LDK, tid);
                 }
                 lds_barrier();
             }
