@@ -121,7 +121,7 @@ __global__ __launch_bounds__(kThreads, 3) void attention_kernel(AttentionArgs p)
             float mx = s[0];
     #pragma unroll
             for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));  // every sub-block holds a valid key of each pair
+            mx = half_pair_max(mx);  // every sub-block holds a valid key of each pair
             // Lazy rescaling: the running max moves only when a score exceeds
             // it by more than kLazy, so weights stay below e^kLazy (well inside
             // f16 for P) and most sub-blocks skip rescaling O entirely.
@@ -141,7 +141,7 @@ __global__ __launch_bounds__(kThreads, 3) void attention_kernel(AttentionArgs p)
                 s[r] = fast_exp2(fmaf(s[r], kLog2e, -mb));
                 sum += s[r];
             }
-            sum += __shfl_xor(sum, 32, 64);
+            sum = half_pair_sum(sum);
             l_run += sum;
             // P^T as the b operand: k-slice element j of this lane is key
             // key0 + 16ks + (j < 4 ? 4hi + j : 8 + 4hi + j - 4); the V^T

@@ -54,10 +54,30 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 // the clobber keeps the compiler from moving LDS accesses across this point.
 __device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
-    return v;
+// x combined with the same register of lane l ^ 32 (the other half of the
+// wave) by v_permlane32_swap, a VALU instruction (__shfl_xor goes through
+// LDS with ds_bpermute). With both operands x, the swap returns for every
+// lane the pair {x[l], x[l ^ 32]} (in lane-half order), so the sum or max
+// of the two results is the pair's, bitwise the same as x + shfl_xor(x, 32).
+// Written as inline assembly: this compiler folds the two results of the
+// builtin into one when both operands hold the same value. The s_nop pair
+// covers the VALU-write -> permlane-read hazard on either side.
+__device__ __forceinline__ void half_pair(float x, float& a, float& b) {
+    a = x;
+    b = x;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+
+__device__ __forceinline__ float half_pair_sum(float x) {
+    float a, b;
+    half_pair(x, a, b);
+    return a + b;
+}
+
+__device__ __forceinline__ float half_pair_max(float x) {
+    float a, b;
+    half_pair(x, a, b);
+    return fmaxf(a, b);
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

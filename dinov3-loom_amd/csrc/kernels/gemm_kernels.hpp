@@ -60,12 +60,12 @@ __device__ __forceinline__ void pair_stats(float* stats, size_t m, int slot, con
     float s = 0.f;
 #pragma unroll
     for (int e = 0; e < 32; ++e) s += v[e];
-    s += __shfl_xor(s, 32, 64);
+    s = half_pair_sum(s);
     const float mean = s * (1.0f / 64.0f);
     float q = 0.f;
 #pragma unroll
     for (int e = 0; e < 32; ++e) q += (v[e] - mean) * (v[e] - mean);
-    q += __shfl_xor(q, 32, 64);
+    q = half_pair_sum(q);
     if (store && hi == 0) *(float2_t*)(stats + m * kStatFloats + slot * 2) = float2_t{mean, q};
 }
 

@@ -36,7 +36,7 @@ __global__ __launch_bounds__(kThreads) void layernorm_kernel(LayerNormArgs p) {
     for (int ks = 0; ks < kLnKs; ++ks)
 #pragma unroll
         for (int e = 0; e < 8; ++e) s += (float)v[ks][e];
-    s += __shfl_xor(s, 32, kWave);
+    s = half_pair_sum(s);
     if (hi == 0) part[0][w][l32] = s;
     __syncthreads();
     // correctly rounded: a constant row's mean is exact
@@ -46,7 +46,7 @@ __global__ __launch_bounds__(kThreads) void layernorm_kernel(LayerNormArgs p) {
     for (int ks = 0; ks < kLnKs; ++ks)
 #pragma unroll
         for (int e = 0; e < 8; ++e) d += ((float)v[ks][e] - mean) * ((float)v[ks][e] - mean);
-    d += __shfl_xor(d, 32, kWave);
+    d = half_pair_sum(d);
     if (hi == 0) part[1][w][l32] = d;
     __syncthreads();
     d = (part[1][0][l32] + part[1][1][l32]) + (part[1][2][l32] + part[1][3][l32]);
@@ -127,12 +127,12 @@ __global__ __launch_bounds__(kThreads) void splitk_reduce_kernel(ReduceArgs p) {
         float s = 0.f;
 #pragma unroll
         for (int e = 0; e < 32; ++e) s += y[e];
-        s += __shfl_xor(s, 32, kWave);
+        s = half_pair_sum(s);
         const float mean = s * (1.0f / 64.0f);
         float q = 0.f;
 #pragma unroll
         for (int e = 0; e < 32; ++e) q += (y[e] - mean) * (y[e] - mean);
-        q += __shfl_xor(q, 32, kWave);
+        q = half_pair_sum(q);
         if (valid && hi == 0) *(float2_t*)(p.stats + (size_t)row * kStatFloats + slot * 2) = float2_t{mean, q};
     }
 }
