@@ -256,6 +256,22 @@ def main():
         roof["avg_us"] = dom["avg_us"]
         model.close()
 
+        # Config 4 beside it: 512x512 (1029 tokens), batch 8, the same weights.
+        hr = d.DINOv3.load(path, d.Options(device=0, max_batch=8, image_size=512))
+        pxh = d.random_pixels(2, 8, 512)
+        trial_hr = {}
+        for nb in ([args.branches] if args.branches else [1, 2]):
+            hr.set_branches(nb)
+            hr.stage(pxh)
+            trial_hr[nb] = timed_replays(hr, 8, 5)
+        branches_hr = min(trial_hr, key=trial_hr.get)
+        hr.set_branches(branches_hr)
+        hr.stage(pxh)
+        for _ in range(5):
+            hr.replay(8)
+        sec_hr = timed_replays(hr, 8, max(10, args.steps // 4))
+        hr.close()
+
         cpu = None if args.no_cpu else cpu_baseline(path, args.cpu_seconds)
 
     for row in table:
@@ -270,6 +286,8 @@ def main():
                    "weights": "seeded random init (BASELINE)"},
         "mfma_frac_forward": round(value * GFLOP_PER_IMAGE / 1e3 / PEAK_TFLOPS, 4),
         "batch32": {"value": round(32 / sec32, 1), "ms_per_step": round(sec32 * 1e3, 4), "branches": branches32},
+        "highres_512_b8": {"value": round(8 / sec_hr, 1), "unit": "images/s", "ms_per_step": round(sec_hr * 1e3, 4),
+                           "branches": branches_hr, "what": "BASELINE.json config 4: 512x512, 1029 tokens, batch 8"},
         "end_to_end": {"value": round(e2e_rate, 1), "unit": "images/s",
                        "what": f"forward() of {4 * b} images from host memory to host memory (PCIe and host copies "
                                f"included, chunks of {b} pipelined); not the metric"},
