@@ -48,9 +48,11 @@ hipError_t launch_resid(const ResidArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_swiglu(const SwigluArgs& a, hipStream_t s) {
-    const int tiles = tiles_for<SwigluTile>(a.rows, 2 * kFF);
-    return a.stats ? launch<SwigluTile>(gemm::swiglu_kernel<SwigluTile, true>, tiles, a, s)
-                   : launch<SwigluTile>(gemm::swiglu_kernel<SwigluTile, false>, tiles, a, s);
+    using T = SwigluTile;
+    const int grid = gemm::tile_grid_split<gemm::kSwigluSlices>((a.rows + T::BM - 1) / T::BM, 2 * kFF / T::BN);
+    if (a.stats) hipLaunchKernelGGL((gemm::swiglu_kernel<T, true>), dim3(grid), dim3(T::THREADS), 0, s, a);
+    else hipLaunchKernelGGL((gemm::swiglu_kernel<T, false>), dim3(grid), dim3(T::THREADS), 0, s, a);
+    return hipGetLastError();
 }
 
 hipError_t launch_splitk(const SplitKArgs& a, hipStream_t s) {

@@ -183,6 +183,29 @@ __device__ __forceinline__ int xcd_tile(int total) {
     return (g >> 3) < per && t < total ? t : -1;
 }
 
+// xcd_tile with the N tiles split into NS slices (NS divides 8 and n_tiles):
+// XCD x takes N slice x % NS over M range x / NS of 8 / NS (n fastest within
+// the XCD, as above). Each XCD's L2 then holds 1/NS of W, which survives the
+// epilogue's output stream, for NS times the A reads. Returns the tile as
+// m_tile * n_tiles + n_tile, or -1.
+template <int NS>
+__device__ __forceinline__ int xcd_tile_split(int m_tiles, int n_tiles) {
+    static_assert(8 % NS == 0, "slices divide the XCDs");
+    constexpr int MS = 8 / NS;
+    const int g = blockIdx.x, x = g & 7, local = g >> 3;
+    const int nsl = n_tiles / NS, mr = x / NS;
+    const int m_lo = mr * m_tiles / MS, m_hi = (mr + 1) * m_tiles / MS;
+    if (local >= (m_hi - m_lo) * nsl) return -1;
+    return (m_lo + local / nsl) * n_tiles + (x % NS) * nsl + local % nsl;
+}
+
+// Workgroups for xcd_tile_split: 8 x the largest XCD share.
+template <int NS>
+inline int tile_grid_split(int m_tiles, int n_tiles) {
+    constexpr int MS = 8 / NS;
+    return 8 * ((m_tiles + MS - 1) / MS) * (n_tiles / NS);
+}
+
 // The pipelined K loop of one tile with P = 2 register sets and two LDS
 // buffers: at step s the workgroup computes stage s from LDS buffer s%2, the
 // loads of stage s+2 go into register set s%2 (whose stage s is already in
@@ -265,10 +288,10 @@ __device__ __forceinline__ void gemm_main(AL (&al)[P], WL (&wl)[P], int m0, int 
 // Issuing the epilogue's loads ahead of the K loop hides their latency, and
 // since they are the oldest loads, the waits that consume them do not wait
 // for the stage loads.
-template <class T, int P, class AL, class WL, class Issue, class Settle, class Epi>
+template <class T, int P, int NS = 1, class AL, class WL, class Issue, class Settle, class Epi>
 __device__ __forceinline__ void gemm_tile(AL (&al)[P], WL (&wl)[P], int n_tiles, int total_tiles, int k_tiles,
                                           half_t* lds, Issue&& issue, Settle&& settle, Epi&& epi) {
-    const int t = xcd_tile(total_tiles);
+    const int t = NS == 1 ? xcd_tile(total_tiles) : xcd_tile_split<NS>(total_tiles / n_tiles, n_tiles);
     if (t < 0) return;  // uniform per workgroup
     const int n0 = (t % n_tiles) * T::BN, m0 = (t / n_tiles) * T::BM;
     issue(m0, n0);

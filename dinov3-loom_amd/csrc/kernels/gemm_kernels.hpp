@@ -294,6 +294,8 @@ __global__ __launch_bounds__(T::THREADS, 4) void resid_kernel(ResidArgs p) {
 // folded LayerNorm) and its rows' statistics are loaded before the K loop;
 // the constants wait in LDS. Each wave stages its TM x 64 block of act in
 // LDS and writes it as whole fragments (act is in fragment order).
+constexpr int kSwigluSlices = 2;  // N slices of the XCD tile split (xcd_tile_split)
+
 template <class T, bool LN>
 __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void swiglu_kernel(SwigluArgs p) {
     static_assert(T::TN % 64 == 0 && T::WGN == 1, "whole gate/up pairs, whole rows per wave");
@@ -311,7 +313,7 @@ __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void swiglu_kernel(
     float4_t raw[T::FM][3];
     RowNorm rn[T::FM];
     float cb = 0.f, cw = 0.f;
-    gemm_tile<T>(
+    gemm_tile<T, 2, kSwigluSlices>(
         al, wl, NT, NT * ((p.rows + T::BM - 1) / T::BM), kHidden / T::BK, lds,
         [&](int m0, int n0) {
             const Frag<T> f(m0, n0);
