@@ -152,12 +152,52 @@ __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void qkv_rope_kerne
     constexpr int SP = T::TN + 8;  // staging pitch in halfs
     constexpr int LDS = T::WAVES * T::TM * SP > 2 * T::W_HALFS ? T::WAVES * T::TM * SP : 2 * T::W_HALFS;
     __shared__ __attribute__((aligned(16))) half_t lds[LDS];
+    __shared__ __attribute__((aligned(16))) float cst[2][T::BN];  // bias, wsum of the tile's columns
+    __shared__ float2_t rows_norm[T::BM];                          // (mean, rstd) of the tile's rows
+    static_assert(T::BN <= T::THREADS, "one thread per column constant");
     const int P = p.grid * p.grid, Tok = P + kPrefix, M = p.images * Tok;
     constexpr int NT = 3 * kHidden / T::BN;
+    const int tid = threadIdx.x;
     ActFrags<T> al[2];
     init_frags(al, p.h, M, kHidden);
     WeightRows<T> wl[2] = {{{}, p.w, kHidden, 0}, {{}, p.w, kHidden, 0}};
-    gemm_tile<T>(al, wl, NT, NT * ((M + T::BM - 1) / T::BM), kHidden / T::BK, lds, [&](const Acc<T>& acc, int m0, int n0) {
+    // The epilogue's own operands are loaded ahead of the K loop and wait in
+    // LDS: the tile's column constants and its rows' LayerNorm (mean, rstd).
+    float4_t raw[T::FM][3];
+    float cb = 0.f, cw = 0.f;
+    gemm_tile<T>(
+        al, wl, NT, NT * ((M + T::BM - 1) / T::BM), kHidden / T::BK, lds,
+        [&](int m0, int n0) {
+            const Frag<T> f(m0, n0);
+            if constexpr (LN) {
+#pragma unroll
+                for (int j = 0; j < T::FM; ++j) {
+                    const float4_t* sp = (const float4_t*)(p.stats + (size_t)min(f.row(j), M - 1) * kStatFloats);
+                    raw[j][0] = sp[0];
+                    raw[j][1] = sp[1];
+                    raw[j][2] = sp[2];
+                }
+            }
+            if (tid < T::BN) {
+                cb = p.bias[n0 + tid];
+                if constexpr (LN) cw = p.wsum[n0 + tid];
+            }
+        },
+        [&] {
+            if (tid < T::BN) {
+                cst[0][tid] = cb;
+                cst[1][tid] = cw;
+            }
+            if constexpr (LN) {
+                const int lane = tid & 63, r0 = (tid >> 6) % T::WGM * T::TM;
+#pragma unroll
+                for (int j = 0; j < T::FM; ++j) {
+                    const RowNorm rn = row_norm(raw[j][0], raw[j][1], raw[j][2]);
+                    if (lane < 32) rows_norm[r0 + j * 32 + lane] = float2_t{rn.mean, rn.rstd};
+                }
+            }
+        },
+        [&](const Acc<T>& acc, int m0, int n0) {
         const Frag<T> f(m0, n0);
         const int lane = threadIdx.x & 63;
         half_t* const st = lds + (threadIdx.x >> 6) * (T::TM * SP);
@@ -186,22 +226,25 @@ __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void qkv_rope_kerne
                     si[g] = float4_t{};
                 }
             }
-            RowNorm rn{0.f, 1.f};
-            if constexpr (LN) rn = row_norm(p.stats, m);
             half_t* const srow = st + (j * 32 + f.l32) * SP;
+            RowNorm rn{0.f, 1.f};
+            if constexpr (LN) {
+                const float2_t v = rows_norm[f.m_base - m0 + j * 32 + f.l32];
+                rn = RowNorm{v[0], v[1]};
+            }
 #pragma unroll
             for (int h2 = 0; h2 < 2; ++h2)
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const int c = g * 8 + f.hi * 4;  // channel in the head (0..31); partner c + 32
-                    const int n = f.n_base + h2 * kHeadDim + c;
+                    const int nl = f.n_base - n0 + h2 * kHeadDim + c;  // column in the tile
                     float4_t lo = group4(acc.v[2 * h2][j], g), up = group4(acc.v[2 * h2 + 1][j], g);
                     if constexpr (LN) {
-                        lo = (lo - rn.mean * ld4(p.wsum + n)) * rn.rstd;
-                        up = (up - rn.mean * ld4(p.wsum + n + 32)) * rn.rstd;
+                        lo = (lo - rn.mean * *(const float4_t*)&cst[1][nl]) * rn.rstd;
+                        up = (up - rn.mean * *(const float4_t*)&cst[1][nl + 32]) * rn.rstd;
                     }
-                    lo += ld4(p.bias + n);
-                    up += ld4(p.bias + n + 32);
+                    lo += *(const float4_t*)&cst[0][nl];
+                    up += *(const float4_t*)&cst[0][nl + 32];
                     const float4_t nlo = lo * co[g] - up * si[g];  // x[c] cos - x[c+32] sin
                     const float4_t nup = up * co[g] + lo * si[g];  // x[c+32] cos + x[c] sin
                     *(half4_t*)(srow + h2 * kHeadDim + c) = to_half4(nlo);
