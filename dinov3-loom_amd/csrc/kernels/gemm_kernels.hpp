@@ -282,39 +282,67 @@ __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void qkv_rope_kerne
 template <class T, bool STATS>
 __global__ __launch_bounds__(T::THREADS, 4) void resid_kernel(ResidArgs p) {
     static_assert(T::TN % 64 == 0 && T::TM == 32, "whole statistics slots, one 32-row block per wave");
+    static_assert(T::BN <= T::THREADS, "one thread per column constant");
     constexpr int SPF = T::TN + 4;  // staging pitch in floats
+    constexpr int XF = T::TN / 16;  // x fragments per wave
     constexpr int LDS = T::WAVES * T::TM * SPF * 2 > 2 * T::W_HALFS ? T::WAVES * T::TM * SPF * 2 : 2 * T::W_HALFS;
     __shared__ __attribute__((aligned(16))) half_t lds[LDS];
+    __shared__ __attribute__((aligned(16))) float cst[2][T::BN];  // bias, ls of the tile's columns
     constexpr int NT = kHidden / T::BN;
+    const int tid = threadIdx.x, lane = tid & 63, mblocks = (p.rows + 31) / 32;
     ActFrags<T> al[2];
     init_frags(al, p.a, p.rows, p.k);
     WeightRows<T> wl[2] = {{{}, p.w, p.k, 0}, {{}, p.w, p.k, 0}};
-    gemm_tile<T>(al, wl, NT, NT * ((p.rows + T::BM - 1) / T::BM), p.k / T::BK, lds,
-                       [&](const Acc<T>& acc, int m0, int n0) {
+    // The epilogue's own operands are loaded ahead of the K loop: the old x
+    // fragments of the wave's 32 x TN block (each x element belongs to one
+    // tile, so nothing else writes them meanwhile) and the column constants
+    // (into LDS).
+    half8_t xold[XF];
+    float cb = 0.f, cl = 0.f;
+    auto x_frag = [&](int m0, int n0, int i) {
+        const Frag<T> f(m0, n0);
+        const int mb = min(f.m_base / 32, mblocks - 1);  // a wave past the rows re-reads the last block
+        return p.x + ((size_t)mb * (kHidden / 16) + f.n_base / 16 + i) * 512 + lane * 8;
+    };
+    gemm_tile<T>(
+        al, wl, NT, NT * ((p.rows + T::BM - 1) / T::BM), p.k / T::BK, lds,
+        [&](int m0, int n0) {
+#pragma unroll
+            for (int i = 0; i < XF; ++i) xold[i] = *(const half8_t*)x_frag(m0, n0, i);
+            if (tid < T::BN) {
+                cb = p.bias[n0 + tid];
+                cl = p.ls[n0 + tid];
+            }
+        },
+        [&] {
+            if (tid < T::BN) {
+                cst[0][tid] = cb;
+                cst[1][tid] = cl;
+            }
+        },
+        [&](const Acc<T>& acc, int m0, int n0) {
         const Frag<T> f(m0, n0);
         float* const st = reinterpret_cast<float*>(lds) + (threadIdx.x >> 6) * (T::TM * SPF);
 #pragma unroll
         for (int i = 0; i < T::FN; ++i)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const int n = f.col(i, g);
-                const float4_t b = ld4(p.bias + n), l = ld4(p.ls + n);
-                *(float4_t*)(st + f.l32 * SPF + (n - f.n_base)) = (group4(acc.v[i][0], g) + b) * l;
+                const int nl = f.col(i, g) - f.n_base;  // column in the wave's TN
+                const int nt = f.n_base - n0 + nl;      // column in the tile
+                const float4_t b = *(const float4_t*)&cst[0][nt], l = *(const float4_t*)&cst[1][nt];
+                *(float4_t*)(st + f.l32 * SPF + nl) = (group4(acc.v[i][0], g) + b) * l;
             }
         wave_lds_sync();
-        const int mb = f.m_base / 32;
-        if (mb >= (p.rows + 31) / 32) return;  // uniform per wave
+        if (f.m_base / 32 >= mblocks) return;  // uniform per wave
         const int m = f.m_base + f.l32;
         const bool valid = m < p.rows;
-        const int lane = threadIdx.x & 63;
 #pragma unroll
         for (int s2 = 0; s2 < T::TN / 64; ++s2) {
             float v[32];
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) {
-                const int c = s2 * 64 + kk * 16 + f.hi * 8;  // column in the wave's 128
-                half_t* const xp = p.x + ((size_t)mb * (kHidden / 16) + (f.n_base + c) / 16) * 512 + lane * 8;
-                const half8_t old = *(const half8_t*)xp;
+                const int c = s2 * 64 + kk * 16 + f.hi * 8;  // column in the wave's TN
+                const half8_t old = xold[s2 * 4 + kk];
                 const float4_t u0 = *(const float4_t*)(st + f.l32 * SPF + c), u1 = *(const float4_t*)(st + f.l32 * SPF + c + 4);
                 half8_t h;
 #pragma unroll
@@ -322,7 +350,7 @@ __global__ __launch_bounds__(T::THREADS, 4) void resid_kernel(ResidArgs p) {
                     h[e] = (half_t)((float)old[e] + u0[e]);
                     h[e + 4] = (half_t)((float)old[e + 4] + u1[e]);
                 }
-                if (valid) *(half8_t*)xp = h;
+                if (valid) *(half8_t*)x_frag(m0, n0, s2 * 4 + kk) = h;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) v[kk * 8 + e] = (float)h[e];
             }
