@@ -1,6 +1,7 @@
 """Build recipe for libdinov3_hrx.so: every HIP kernel and host source is
 compiled with hipcc for gfx950 (wave64) and linked into one shared library
-that exports the C ABI of include/dinov3.h and include/dinov3_engine.h.
+that exports the C ABI of include/dinov3.h and include/dinov3_engine.h; the
+command-line front end lib/dinov3-hrx (csrc/cli.cpp) links against it.
 
     python dinov3-loom_amd/build.py [-j N]
 """
@@ -17,6 +18,7 @@ CSRC = os.path.join(HERE, "csrc")
 LIB_DIR = os.path.join(HERE, "lib")
 OBJ_DIR = os.path.join(LIB_DIR, "obj")
 LIB_PATH = os.path.join(LIB_DIR, "libdinov3_hrx.so")
+CLI_PATH = os.path.join(LIB_DIR, "dinov3-hrx")
 
 SOURCES = [
     "kernels/gemm.hip",
@@ -79,7 +81,19 @@ def build(jobs: int = 8, verbose: bool = False) -> str:
     link = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *[o for _, o in cmds], "-o", tmp]
     subprocess.check_call(link)
     os.replace(tmp, LIB_PATH)
+    build_cli()
     return LIB_PATH
+
+
+def build_cli() -> str:
+    """The command-line front end (csrc/cli.cpp, host code only) linked
+    against the library next to it."""
+    tmp = CLI_PATH + ".tmp"
+    subprocess.check_call([os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-Wall", "-I", os.path.join(ROOT, "include"),
+                           os.path.join(CSRC, "cli.cpp"), "-L", LIB_DIR, "-ldinov3_hrx", "-Wl,-rpath,$ORIGIN",
+                           "-o", tmp])
+    os.replace(tmp, CLI_PATH)
+    return CLI_PATH
 
 
 if __name__ == "__main__":
