@@ -12,6 +12,8 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float2_t __attribute__((ext_vector_type(2)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef float float16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t uint2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t uint4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kHidden = 384;
 constexpr int kHeads = 6;
@@ -78,6 +80,38 @@ __device__ __forceinline__ float half_pair_max(float x) {
     float a, b;
     half_pair(x, a, b);
     return fmaxf(a, b);
+}
+
+// Fragment order from a 32x32 MFMA result. Lane (l, hi) of the result holds
+// row l, columns 8g + 4hi .. +3 in register group g; fragment order wants
+// lane (l, hi) to hold columns 8hi .. 8hi+7 of each 16-column block. For
+// the block of groups (g0, g1) = (2kk, 2kk+1) that is one exchange: the
+// upper half-wave's g0 values swap with the lower half-wave's g1 values
+// (v_permlane32_swap), after which every lane holds its 8 columns as
+// {g0, g1}. These take the groups' values as 32-bit words (4 f32 values,
+// or 4 f16 values packed in 2 words).
+__device__ __forceinline__ void frag_swap(float4_t& g0, float4_t& g1) {
+    float a0 = g0[0], a1 = g0[1], a2 = g0[2], a3 = g0[3], b0 = g1[0], b1 = g1[1], b2 = g1[2], b3 = g1[3];
+    asm("s_nop 1\n\t"
+        "v_permlane32_swap_b32 %0, %4\n\t"
+        "v_permlane32_swap_b32 %1, %5\n\t"
+        "v_permlane32_swap_b32 %2, %6\n\t"
+        "v_permlane32_swap_b32 %3, %7\n\t"
+        "s_nop 1"
+        : "+v"(a0), "+v"(a1), "+v"(a2), "+v"(a3), "+v"(b0), "+v"(b1), "+v"(b2), "+v"(b3));
+    g0 = float4_t{a0, a1, a2, a3};
+    g1 = float4_t{b0, b1, b2, b3};
+}
+
+__device__ __forceinline__ half8_t frag_swap(half4_t g0, half4_t g1) {
+    uint2_t a = __builtin_bit_cast(uint2_t, g0), b = __builtin_bit_cast(uint2_t, g1);
+    uint32_t a0 = a[0], a1 = a[1], b0 = b[0], b1 = b[1];
+    asm("s_nop 1\n\t"
+        "v_permlane32_swap_b32 %0, %2\n\t"
+        "v_permlane32_swap_b32 %1, %3\n\t"
+        "s_nop 1"
+        : "+v"(a0), "+v"(a1), "+v"(b0), "+v"(b1));
+    return __builtin_bit_cast(half8_t, uint4_t{a0, a1, b0, b1});
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

@@ -277,16 +277,16 @@ __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void qkv_rope_kerne
 
 // Residual GEMM: x += ls * (A W^T + b), in place on the f16 residual stream
 // in fragment order (with STATS, also the LayerNorm row statistics of the
-// updated x). Each wave stages its f32 update (32 x TN) in LDS, then reads
-// and writes x fragment by fragment (1 KB contiguous per wave access).
+// updated x). The epilogue turns each 16-column half of an MFMA result into a
+// fragment in registers (frag_swap) and reads and writes x fragment by
+// fragment (1 KB contiguous per wave access); LDS holds only the weight
+// stages and the column constants.
 template <class T, bool STATS>
 __global__ __launch_bounds__(T::THREADS, 4) void resid_kernel(ResidArgs p) {
     static_assert(T::TN % 64 == 0 && T::TM == 32, "whole statistics slots, one 32-row block per wave");
     static_assert(T::BN <= T::THREADS, "one thread per column constant");
-    constexpr int SPF = T::TN + 4;  // staging pitch in floats
     constexpr int XF = T::TN / 16;  // x fragments per wave
-    constexpr int LDS = T::WAVES * T::TM * SPF * 2 > 2 * T::W_HALFS ? T::WAVES * T::TM * SPF * 2 : 2 * T::W_HALFS;
-    __shared__ __attribute__((aligned(16))) half_t lds[LDS];
+    __shared__ __attribute__((aligned(16))) half_t lds[2 * T::W_HALFS];
     __shared__ __attribute__((aligned(16))) float cst[2][T::BN];  // bias, ls of the tile's columns
     constexpr int NT = kHidden / T::BN;
     const int tid = threadIdx.x, lane = tid & 63, mblocks = (p.rows + 31) / 32;
@@ -322,17 +322,6 @@ __global__ __launch_bounds__(T::THREADS, 4) void resid_kernel(ResidArgs p) {
         },
         [&](const Acc<T>& acc, int m0, int n0) {
         const Frag<T> f(m0, n0);
-        float* const st = reinterpret_cast<float*>(lds) + (threadIdx.x >> 6) * (T::TM * SPF);
-#pragma unroll
-        for (int i = 0; i < T::FN; ++i)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int nl = f.col(i, g) - f.n_base;  // column in the wave's TN
-                const int nt = f.n_base - n0 + nl;      // column in the tile
-                const float4_t b = *(const float4_t*)&cst[0][nt], l = *(const float4_t*)&cst[1][nt];
-                *(float4_t*)(st + f.l32 * SPF + nl) = (group4(acc.v[i][0], g) + b) * l;
-            }
-        wave_lds_sync();
         if (f.m_base / 32 >= mblocks) return;  // uniform per wave
         const int m = f.m_base + f.l32;
         const bool valid = m < p.rows;
@@ -340,19 +329,30 @@ __global__ __launch_bounds__(T::THREADS, 4) void resid_kernel(ResidArgs p) {
         for (int s2 = 0; s2 < T::TN / 64; ++s2) {
             float v[32];
 #pragma unroll
-            for (int kk = 0; kk < 4; ++kk) {
-                const int c = s2 * 64 + kk * 16 + f.hi * 8;  // column in the wave's TN
-                const half8_t old = xold[s2 * 4 + kk];
-                const float4_t u0 = *(const float4_t*)(st + f.l32 * SPF + c), u1 = *(const float4_t*)(st + f.l32 * SPF + c + 4);
-                half8_t h;
+            for (int i2 = 0; i2 < 2; ++i2) {
+                const int i = 2 * s2 + i2;  // 32-column MFMA tile of the wave
+                float4_t u[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    h[e] = (half_t)((float)old[e] + u0[e]);
-                    h[e + 4] = (half_t)((float)old[e + 4] + u1[e]);
+                for (int g = 0; g < 4; ++g) {
+                    const int nt = f.col(i, g) - n0;  // column in the tile
+                    const float4_t b = *(const float4_t*)&cst[0][nt], l = *(const float4_t*)&cst[1][nt];
+                    u[g] = (group4(acc.v[i][0], g) + b) * l;
                 }
-                if (valid) *(half8_t*)x_frag(m0, n0, s2 * 4 + kk) = h;
+                frag_swap(u[0], u[1]);
+                frag_swap(u[2], u[3]);
 #pragma unroll
-                for (int e = 0; e < 8; ++e) v[kk * 8 + e] = (float)h[e];
+                for (int kk = 0; kk < 2; ++kk) {
+                    const half8_t old = xold[2 * i + kk];
+                    half8_t h;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        h[e] = (half_t)((float)old[e] + u[2 * kk][e]);
+                        h[e + 4] = (half_t)((float)old[e + 4] + u[2 * kk + 1][e]);
+                    }
+                    if (valid) *(half8_t*)x_frag(m0, n0, 2 * i + kk) = h;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) v[(i2 * 2 + kk) * 8 + e] = (float)h[e];
+                }
             }
             if constexpr (STATS) pair_stats(p.stats, m, f.n_base / 64 + s2, v, f.hi, valid);
         }
@@ -363,18 +363,16 @@ __global__ __launch_bounds__(T::THREADS, 4) void resid_kernel(ResidArgs p) {
 // the 32 matching up rows, so a wave's 128 columns are two gate/up pairs of
 // 32 outputs each. The tile's column constants (bias, and wsum with the
 // folded LayerNorm) and its rows' statistics are loaded before the K loop;
-// the constants wait in LDS. Each wave stages its TM x 64 block of act in
-// LDS and writes it as whole fragments (act is in fragment order).
+// the constants wait in LDS. The epilogue turns each 16-column half of a
+// 32-column act block into a fragment in registers (frag_swap) and writes
+// it whole (act is in fragment order).
 constexpr int kSwigluSlices = 2;  // N slices of the XCD tile split (xcd_tile_split)
 
 template <class T, bool LN>
 __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void swiglu_kernel(SwigluArgs p) {
     static_assert(T::TN % 64 == 0 && T::WGN == 1, "whole gate/up pairs, whole rows per wave");
     static_assert(T::BN <= T::THREADS, "one thread per column constant");
-    constexpr int OW = T::TN / 2;  // act columns per wave
-    constexpr int SP = OW + 8;     // staging pitch in halfs
-    constexpr int LDS = T::WAVES * T::TM * SP > 2 * T::W_HALFS ? T::WAVES * T::TM * SP : 2 * T::W_HALFS;
-    __shared__ __attribute__((aligned(16))) half_t lds[LDS];
+    __shared__ __attribute__((aligned(16))) half_t lds[2 * T::W_HALFS];
     __shared__ __attribute__((aligned(16))) float cst[2][T::BN];  // bias, wsum
     constexpr int NT = 2 * kFF / T::BN;
     const int tid = threadIdx.x;
@@ -412,13 +410,16 @@ __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void swiglu_kernel(
         },
         [&](const Acc<T>& acc, int m0, int n0) {
         const Frag<T> f(m0, n0);
-        half_t* const st = lds + (threadIdx.x >> 6) * T::TM * SP;
+        const int lane = threadIdx.x & 63, mblocks = (p.rows + 31) / 32;
         // Pair q of the wave: gate = acc.v[2q], up = acc.v[2q + 1], outputs
-        // 32q .. 32q+31 of the wave's OW.
+        // 32q .. 32q+31 of the wave's OW, i.e. act fragments 2q and 2q + 1.
 #pragma unroll
         for (int j = 0; j < T::FM; ++j) {
+            const int mb = f.m_base / 32 + j;
+            if (mb >= mblocks) break;  // uniform per wave
 #pragma unroll
-            for (int q = 0; q < T::FN / 2; ++q)
+            for (int q = 0; q < T::FN / 2; ++q) {
+                half4_t y[4];
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const int c = g * 8 + f.hi * 4, nl = f.n_base - n0 + 64 * q + c;
@@ -429,20 +430,13 @@ __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void swiglu_kernel(
                     }
                     gate += *(const float4_t*)&cst[0][nl];
                     up += *(const float4_t*)&cst[0][nl + 32];
-                    const float4_t y = float4_t{silu(gate[0]), silu(gate[1]), silu(gate[2]), silu(gate[3])} * up;
-                    *(half4_t*)(st + (j * 32 + f.l32) * SP + 32 * q + c) = to_half4(y);
+                    y[g] = to_half4(float4_t{silu(gate[0]), silu(gate[1]), silu(gate[2]), silu(gate[3])} * up);
                 }
-        }
-        wave_lds_sync();
-        const int lane = threadIdx.x & 63, mblocks = (p.rows + 31) / 32;
 #pragma unroll
-        for (int j = 0; j < T::FM; ++j) {
-            const int mb = f.m_base / 32 + j;
-            if (mb >= mblocks) break;  // uniform per wave
-#pragma unroll
-            for (int ks = 0; ks < OW / 16; ++ks)
-                *(half8_t*)(p.act + ((size_t)mb * (kFF / 16) + f.n_base / 32 + ks) * 512 + lane * 8) =
-                    *(const half8_t*)(st + (j * 32 + f.l32) * SP + ks * 16 + f.hi * 8);
+                for (int kk = 0; kk < 2; ++kk)
+                    *(half8_t*)(p.act + ((size_t)mb * (kFF / 16) + f.n_base / 32 + 2 * q + kk) * 512 + lane * 8) =
+                        frag_swap(y[2 * kk], y[2 * kk + 1]);
+            }
         }
     });
 }
