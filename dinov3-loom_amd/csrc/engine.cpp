@@ -141,7 +141,7 @@ Need required(const dhx_launch& l) {
         case DHX_K_RESID:
         case DHX_K_RESID_STATS: {
             positive(s[0], "rows");
-            if (s[1] == 0 || s[1] % 128 != 0) throw dhx::Error("k must be a positive multiple of 128");
+            if (s[1] == 0 || s[1] % 384 != 0) throw dhx::Error("k must be a positive multiple of 384");
             std::vector<uint64_t> b = {frag(s[0], s[1]), H * s[1] * 2, H * 4, H * 4, frag(s[0], H)};
             if (l.kernel == DHX_K_RESID_STATS) b.push_back(s[0] * S);
             return {(uint32_t)b.size(), b};
@@ -156,7 +156,7 @@ Need required(const dhx_launch& l) {
         case DHX_K_SPLITK: {
             positive(s[0], "rows");
             positive(s[2], "splits");
-            if (s[1] == 0 || s[1] % (128ull * s[2]) != 0) throw dhx::Error("k must split into multiples of 128");
+            if (s[1] == 0 || s[1] % (384ull * s[2]) != 0) throw dhx::Error("k must split into multiples of 384");
             return {3, {frag(s[0], s[1]), H * s[1] * 2, (uint64_t)s[2] * s[0] * H * 4}};
         }
         case DHX_K_SPLITK_REDUCE:

@@ -22,6 +22,10 @@ constexpr int kPrefix = 5;
 constexpr int kFF = 1536;
 constexpr int kWave = 64;
 constexpr float kLog2e = 1.4426950408889634f;
+// Word 3 of a raw buffer descriptor on CDNA (gfx9 family): 32-bit data
+// format (untyped buffer instructions need a nonzero one), no swizzle, no
+// index stride.
+constexpr int kBufferRsrcWord3 = 0x00020000;
 
 // v_mfma_f32_32x32x16_f16. Operand a: lane l holds row (l % 32), k-slice
 // 8*(l / 32) .. +7; operand b: lane l holds column (l % 32), the same

@@ -40,8 +40,8 @@ hipError_t launch_qkv_rope(const QkvArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_resid(const ResidArgs& a, hipStream_t s) {
-    // The K loop walks its stages two at a time.
-    if (a.k % (2 * ResidTile::BK) != 0) return hipErrorInvalidValue;
+    // The K loop walks its stages six at a time (gemm_main_dma).
+    if (a.k % (6 * ResidTile::BK) != 0) return hipErrorInvalidValue;
     const int tiles = tiles_for<ResidTile>(a.rows, kHidden);
     return a.stats ? launch<ResidTile>(gemm::resid_kernel<ResidTile, true>, tiles, a, s)
                    : launch<ResidTile>(gemm::resid_kernel<ResidTile, false>, tiles, a, s);
@@ -49,6 +49,7 @@ hipError_t launch_resid(const ResidArgs& a, hipStream_t s) {
 
 hipError_t launch_swiglu(const SwigluArgs& a, hipStream_t s) {
     using T = SwigluTile;
+    static_assert(kHidden % (6 * T::BK) == 0, "the K loop walks its stages six at a time");
     const int grid = gemm::tile_grid_split<gemm::kSwigluSlices>((a.rows + T::BM - 1) / T::BM, 2 * kFF / T::BN);
     if (a.stats) hipLaunchKernelGGL((gemm::swiglu_kernel<T, true>), dim3(grid), dim3(T::THREADS), 0, s, a);
     else hipLaunchKernelGGL((gemm::swiglu_kernel<T, false>), dim3(grid), dim3(T::THREADS), 0, s, a);
@@ -56,6 +57,8 @@ hipError_t launch_swiglu(const SwigluArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_splitk(const SplitKArgs& a, hipStream_t s) {
+    // Each split's K loop walks its stages six at a time (gemm_main_dma).
+    if (a.splits < 1 || a.k % a.splits != 0 || (a.k / a.splits) % (6 * SplitTile::BK) != 0) return hipErrorInvalidValue;
     return launch<SplitTile>(gemm::splitk_kernel<SplitTile>, tiles_for<SplitTile>(a.rows, kHidden) * a.splits, a, s);
 }
 

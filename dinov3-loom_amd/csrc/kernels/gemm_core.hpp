@@ -39,6 +39,7 @@ struct Tile {
     static constexpr int FM = TM / 32, FN = TN / 32;
     static constexpr int STAGE_HALFS = (BM + BN) * LDK;
     static constexpr int W_HALFS = BN * LDK;  // weight-only stage (activations in registers)
+    static constexpr int WF_HALFS = BN * BK;  // weight-only stage in fragment order (WeightDma)
     static constexpr int LDS_HALFS = 2 * STAGE_HALFS;
     static constexpr int LDS_BYTES = LDS_HALFS * 2;
 };
@@ -115,6 +116,41 @@ struct ActFrags {
     }
 };
 
+// Weight operand in fragment order, moved from global memory straight into
+// LDS. W[N][K] is stored as 32-row x 16-column blocks (the layout of
+// fragment-order activations, common.hpp: block (nb, ks) at
+// (nb * K/16 + ks) * 512 halfs, lane hi*32 + l holding row l, columns
+// 8hi .. 8hi+7). buffer_load_dwordx4 with the lds flag writes each lane's
+// 16 bytes to M0 + 16 * lane, so one instruction moves one 1 KB block and
+// the LDS stage keeps the fragment order: block (nb, ks) of the stage at
+// (nb * BK/16 + ks) * 512 halfs, read back conflict-free with
+// ds_read_b128. No registers, no ds_write. The stage's blocks are split
+// evenly over the waves. The buffer descriptor bounds every access to W.
+template <class T>
+struct WeightDma {
+    static constexpr int KS = T::BK / 16;
+    static constexpr int BLOCKS = T::BN / 32 * KS;  // per stage
+    static constexpr int PER_WAVE = BLOCKS / T::WAVES;
+    static_assert(BLOCKS % T::WAVES == 0, "whole blocks per wave");
+    __amdgpu_buffer_rsrc_t rsrc;
+    int ksteps;  // K / 16 of W
+    int ks_off;  // first k-step (split-K)
+    __device__ __forceinline__ WeightDma(const half_t* w, int n, int k)
+        : rsrc(__builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(w), 0, n * k * 2, kBufferRsrcWord3)),
+          ksteps(k / 16),
+          ks_off(0) {}
+    __device__ __forceinline__ void load(half_t* stage, int n0, int kt, int tid) const {
+        const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+#pragma unroll
+        for (int b = 0; b < PER_WAVE; ++b) {
+            const int blk = wave * PER_WAVE + b, nb = blk / KS, ks = blk % KS;
+            const int off = (((n0 >> 5) + nb) * ksteps + ks_off + kt * KS + ks) * 1024;  // uniform
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)(stage + blk * 512),
+                                                     16, (tid & 63) * 16, off, 0, 0);
+        }
+    }
+};
+
 template <class T>
 struct Acc {
     float16_t v[T::FN][T::FM];
@@ -164,6 +200,29 @@ __device__ __forceinline__ void mma_stage_areg(const half_t* stage, int tid, con
 #pragma unroll
     for (int kk = 0; kk < T::BK / 16; ++kk) {
         if (kk + 1 < T::BK / 16) fetch(kk + 1, (kk + 1) & 1);
+#pragma unroll
+        for (int i = 0; i < T::FN; ++i)
+#pragma unroll
+            for (int j = 0; j < T::FM; ++j) acc.v[i][j] = mfma32x32x16(wf[kk & 1][i], af.f[j][kk], acc.v[i][j]);
+    }
+}
+
+// mma_stage_areg with the weight stage in fragment order (WeightDma): the
+// wave reads every column of the stage (WGN == 1), one contiguous 1 KB block
+// per fragment.
+template <class T, class AF>
+__device__ __forceinline__ void mma_stage_frag(const half_t* stage, int tid, const AF& af, Acc<T>& acc) {
+    constexpr int KS = T::BK / 16;
+    const half_t* w_s = stage + (tid & 63) * 8;
+    half8_t wf[2][T::FN];
+    auto fetch = [&](int kk, int b) {
+#pragma unroll
+        for (int i = 0; i < T::FN; ++i) wf[b][i] = *(const half8_t*)(w_s + (i * KS + kk) * 512);
+    };
+    fetch(0, 0);
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+        if (kk + 1 < KS) fetch(kk + 1, (kk + 1) & 1);
 #pragma unroll
         for (int i = 0; i < T::FN; ++i)
 #pragma unroll
@@ -305,6 +364,80 @@ template <class T, int P, class AL, class WL, class Epi>
 __device__ __forceinline__ void gemm_tile(AL (&al)[P], WL (&wl)[P], int n_tiles, int total_tiles, int k_tiles,
                                           half_t* lds, Epi&& epi) {
     gemm_tile<T, P>(al, wl, n_tiles, total_tiles, k_tiles, lds, [](int, int) {}, [] {}, epi);
+}
+
+// Waits until at most N of this wave's vector-memory operations are
+// outstanding and its LDS traffic is done, then joins the workgroup barrier.
+// Vector-memory operations complete in issue order, LDS DMA included.
+template <int N>
+__device__ __forceinline__ void vm_barrier() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// The K loop with activations in registers (two sets, ActFrags) and the
+// weight stages moved into three LDS buffers by DMA (WeightDma). At step s
+// the DMA of stage s+2 goes into the buffer that held stage s-1 (read by
+// every wave before the previous barrier), stage s is computed from its
+// buffer, and register set s%2 is refilled with stage s+2. The barrier that
+// ends step s waits for everything but this step's own loads, so stage s+1
+// has landed in LDS for every wave. The three buffers are separate LDS
+// variables and the loop is unrolled over them, so the compiler can tell a
+// buffer being read from the ones being filled and does not wait for the
+// DMA in flight. DMA stops at the last stage (nothing lands in LDS after
+// the loop); activation loads past it repeat the last stage. k_tiles must be
+// a multiple of 6 (the launchers check).
+template <class T, class AL, class WD, class Settle>
+__device__ __forceinline__ void gemm_main_dma(AL (&al)[2], const WD& wd, half_t* b0, half_t* b1, half_t* b2, int m0,
+                                              int n0, int k_tiles, Acc<T>& acc, Settle&& settle) {
+    static_assert(AL::kInRegs, "activations in registers");
+    constexpr int NA = T::FM * (T::BK / 16), NW = WD::PER_WAVE;
+    const int tid = threadIdx.x, last = k_tiles - 1;
+#pragma unroll
+    for (int i = 0; i < T::FN; ++i)
+#pragma unroll
+        for (int j = 0; j < T::FM; ++j) acc.v[i][j] = float16_t{};
+    al[0].load(m0, n0, 0, tid);
+    wd.load(b0, n0, 0, tid);
+    al[1].load(m0, n0, min(1, last), tid);
+    if (k_tiles > 1) wd.load(b1, n0, 1, tid);
+    settle();
+    if (k_tiles > 1)
+        vm_barrier<NA + NW>();
+    else
+        vm_barrier<NA>();
+    auto step = [&](const half_t* cur, half_t* fill, AL& a, int s) {
+        const bool more = s + 2 < k_tiles;  // uniform
+        if (more) wd.load(fill, n0, s + 2, tid);
+        mma_stage_frag<T>(cur, tid, a, acc);
+        a.load(m0, n0, min(s + 2, last), tid);
+        if (more)
+            vm_barrier<NA + NW>();
+        else
+            vm_barrier<NA>();
+    };
+    for (int kt = 0; kt < k_tiles; kt += 6) {
+        step(b0, b2, al[0], kt);
+        step(b1, b0, al[1], kt + 1);
+        step(b2, b1, al[0], kt + 2);
+        step(b0, b2, al[1], kt + 3);
+        step(b1, b0, al[0], kt + 4);
+        step(b2, b1, al[1], kt + 5);
+    }
+}
+
+// gemm_tile over gemm_main_dma.
+template <class T, int NS = 1, class AL, class WD, class Issue, class Settle, class Epi>
+__device__ __forceinline__ void gemm_tile_dma(AL (&al)[2], WD& wd, half_t* b0, half_t* b1, half_t* b2, int n_tiles,
+                                              int total_tiles, int k_tiles, Issue&& issue, Settle&& settle,
+                                              Epi&& epi) {
+    const int t = NS == 1 ? xcd_tile(total_tiles) : xcd_tile_split<NS>(total_tiles / n_tiles, n_tiles);
+    if (t < 0) return;  // uniform per workgroup
+    const int n0 = (t % n_tiles) * T::BN, m0 = (t / n_tiles) * T::BM;
+    issue(m0, n0);
+    Acc<T> acc;
+    gemm_main_dma<T>(al, wd, b0, b1, b2, m0, n0, k_tiles, acc, settle);
+    epi(acc, m0, n0);
 }
 
 // Workgroups for a launch: one per tile (a persistent walk over several

@@ -286,13 +286,13 @@ __global__ __launch_bounds__(T::THREADS, 4) void resid_kernel(ResidArgs p) {
     static_assert(T::TN % 64 == 0 && T::TM == 32, "whole statistics slots, one 32-row block per wave");
     static_assert(T::BN <= T::THREADS, "one thread per column constant");
     constexpr int XF = T::TN / 16;  // x fragments per wave
-    __shared__ __attribute__((aligned(16))) half_t lds[2 * T::W_HALFS];
+    __shared__ __attribute__((aligned(16))) half_t wb0[T::WF_HALFS], wb1[T::WF_HALFS], wb2[T::WF_HALFS];
     __shared__ __attribute__((aligned(16))) float cst[2][T::BN];  // bias, ls of the tile's columns
     constexpr int NT = kHidden / T::BN;
     const int tid = threadIdx.x, lane = tid & 63, mblocks = (p.rows + 31) / 32;
     ActFrags<T> al[2];
     init_frags(al, p.a, p.rows, p.k);
-    WeightRows<T> wl[2] = {{{}, p.w, p.k, 0}, {{}, p.w, p.k, 0}};
+    WeightDma<T> wd(p.w, kHidden, p.k);
     // The epilogue's own operands are loaded ahead of the K loop: the old x
     // fragments of the wave's 32 x TN block (each x element belongs to one
     // tile, so nothing else writes them meanwhile) and the column constants
@@ -304,8 +304,8 @@ __global__ __launch_bounds__(T::THREADS, 4) void resid_kernel(ResidArgs p) {
         const int mb = min(f.m_base / 32, mblocks - 1);  // a wave past the rows re-reads the last block
         return p.x + ((size_t)mb * (kHidden / 16) + f.n_base / 16 + i) * 512 + lane * 8;
     };
-    gemm_tile<T>(
-        al, wl, NT, NT * ((p.rows + T::BM - 1) / T::BM), p.k / T::BK, lds,
+    gemm_tile_dma<T>(
+        al, wd, wb0, wb1, wb2, NT, NT * ((p.rows + T::BM - 1) / T::BM), p.k / T::BK,
         [&](int m0, int n0) {
 #pragma unroll
             for (int i = 0; i < XF; ++i) xold[i] = *(const half8_t*)x_frag(m0, n0, i);
@@ -372,18 +372,18 @@ template <class T, bool LN>
 __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void swiglu_kernel(SwigluArgs p) {
     static_assert(T::TN % 64 == 0 && T::WGN == 1, "whole gate/up pairs, whole rows per wave");
     static_assert(T::BN <= T::THREADS, "one thread per column constant");
-    __shared__ __attribute__((aligned(16))) half_t lds[2 * T::W_HALFS];
+    __shared__ __attribute__((aligned(16))) half_t wb0[T::WF_HALFS], wb1[T::WF_HALFS], wb2[T::WF_HALFS];
     __shared__ __attribute__((aligned(16))) float cst[2][T::BN];  // bias, wsum
     constexpr int NT = 2 * kFF / T::BN;
     const int tid = threadIdx.x;
     ActFrags<T> al[2];
     init_frags(al, p.h, p.rows, kHidden);
-    WeightRows<T> wl[2] = {{{}, p.w, kHidden, 0}, {{}, p.w, kHidden, 0}};
+    WeightDma<T> wd(p.w, 2 * kFF, kHidden);
     float4_t raw[T::FM][3];
     RowNorm rn[T::FM];
     float cb = 0.f, cw = 0.f;
-    gemm_tile<T, 2, kSwigluSlices>(
-        al, wl, NT, NT * ((p.rows + T::BM - 1) / T::BM), kHidden / T::BK, lds,
+    gemm_tile_dma<T, kSwigluSlices>(
+        al, wd, wb0, wb1, wb2, NT, NT * ((p.rows + T::BM - 1) / T::BM), kHidden / T::BK,
         [&](int m0, int n0) {
             const Frag<T> f(m0, n0);
             if constexpr (LN) {
@@ -462,37 +462,29 @@ struct SplitActFrags : ActFrags<T> {
 };
 
 template <class T>
-struct SplitWeightRows {
-    WeightRows<T> w;
-    SplitDecode<T> d;
-    __device__ __forceinline__ void load(int m0, int n0, int kt, int tid) {
-        w.k_off = d.split(m0) * d.kc;
-        w.load(m0, n0, kt, tid);
-    }
-    __device__ __forceinline__ void store(half_t* s, int tid) const { w.store(s, tid); }
-};
-
-template <class T>
 __global__ __launch_bounds__(T::THREADS, 3) void splitk_kernel(SplitKArgs p) {
-    __shared__ __attribute__((aligned(16))) half_t lds[2 * T::W_HALFS];
+    __shared__ __attribute__((aligned(16))) half_t wb0[T::WF_HALFS], wb1[T::WF_HALFS], wb2[T::WF_HALFS];
     constexpr int NT = kHidden / T::BN;
     const int MT = (p.rows + T::BM - 1) / T::BM;
     const SplitDecode<T> d{MT, p.k / p.splits};
     ActFrags<T> base[2];
     init_frags(base, p.a, p.rows, p.k);
     SplitActFrags<T> al[2] = {{base[0], d}, {base[1], d}};
-    SplitWeightRows<T> wl[2] = {{{{}, p.w, p.k, 0}, d}, {{{}, p.w, p.k, 0}, d}};
-    gemm_tile<T>(al, wl, NT, NT * MT * p.splits, d.kc / T::BK, lds, [&](const Acc<T>& acc, int m0, int n0) {
-        const Frag<T> f(d.row0(m0), n0);
-        float* slab = p.partials + (size_t)d.split(m0) * p.rows * kHidden;
-        const int m = f.row(0);
-        if (m >= p.rows) return;
+    WeightDma<T> wd(p.w, kHidden, p.k);
+    gemm_tile_dma<T>(
+        al, wd, wb0, wb1, wb2, NT, NT * MT * p.splits, d.kc / T::BK,
+        [&](int m0, int) { wd.ks_off = d.split(m0) * (d.kc / 16); }, [] {},
+        [&](const Acc<T>& acc, int m0, int n0) {
+            const Frag<T> f(d.row0(m0), n0);
+            float* slab = p.partials + (size_t)d.split(m0) * p.rows * kHidden;
+            const int m = f.row(0);
+            if (m >= p.rows) return;
 #pragma unroll
-        for (int i = 0; i < T::FN; ++i)
+            for (int i = 0; i < T::FN; ++i)
 #pragma unroll
-            for (int g = 0; g < 4; ++g)
-                *(float4_t*)(slab + (size_t)m * kHidden + f.col(i, g)) = group4(acc.v[i][0], g);
-    });
+                for (int g = 0; g < 4; ++g)
+                    *(float4_t*)(slab + (size_t)m * kHidden + f.col(i, g)) = group4(acc.v[i][0], g);
+        });
 }
 
 }  // namespace gemm

@@ -80,6 +80,20 @@ Folded fold_layernorm(const std::string& name, const std::vector<float>& w, cons
 
 std::vector<float> prefix_stats(const std::vector<float>& prefix);
 
+// Row-major f16 [n][k] -> the fragment order the GEMMs' weight DMA reads:
+// 32-row x 16-column blocks, block (nb, ks) at (nb * k/16 + ks) * 512
+// halfs, lane hi*32 + l of a block holding row 32nb + l, columns
+// 16ks + 8hi .. +7 (n a multiple of 32, k of 16).
+std::vector<uint8_t> fragment_order(const std::vector<uint8_t>& rows, size_t n, size_t k) {
+    std::vector<uint8_t> out(rows.size());
+    for (size_t r = 0; r < n; ++r)
+        for (size_t c8 = 0; c8 < k; c8 += 8) {
+            const size_t dst = ((r / 32) * (k / 16) + c8 / 16) * 512 + ((c8 / 8) % 2 * 32 + r % 32) * 8;
+            std::memcpy(&out[dst * 2], &rows[(r * k + c8) * 2], 16);
+        }
+    return out;
+}
+
 }  // namespace
 
 std::vector<uint8_t> pack_f16(const std::string& name, const float* values, size_t n) {
@@ -195,18 +209,20 @@ Packed load_weights(const std::string& path, uint32_t grid) {
                 b[blk * 64 + r] = gb[src];
                 b[blk * 64 + 32 + r] = ub[src];
             }
-        emit(l + "gateup_w", w, true);
+        out.emplace_back(l + "gateup_w", fragment_order(pack_f16(l + "gateup_w", w.data(), w.size()), 3072, 384));
         emit(l + "gateup_b", b, false);
         {
             Folded f = fold_layernorm(l + "gateup_wln", w, b, get(st, p + "norm2.weight", {384}),
                                       get(st, p + "norm2.bias", {384}), 3072, 384);
-            out.emplace_back(l + "gateup_wln", std::move(f.w));
+            out.emplace_back(l + "gateup_wln", fragment_order(f.w, 3072, 384));
             emit(l + "gateup_wsum", f.wsum, false);
             emit(l + "gateup_t", f.t, false);
         }
         for (auto& v : {std::make_pair("o", std::make_pair("attention.o_proj", 384u)),
                         std::make_pair("down", std::make_pair("mlp.down_proj", 1536u))}) {
-            emit(l + v.first + "_w", get(st, p + v.second.first + ".weight", {384, v.second.second}), true);
+            const std::vector<float> w = get(st, p + v.second.first + ".weight", {384, v.second.second});
+            out.emplace_back(l + v.first + "_w",
+                             fragment_order(pack_f16(l + v.first + "_w", w.data(), w.size()), 384, v.second.second));
             emit(l + v.first + "_b", get(st, p + v.second.first + ".bias", {384}), false);
         }
     }

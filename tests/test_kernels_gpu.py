@@ -277,7 +277,7 @@ def test_resid(eng, rows, kdim):
     ls = rng.uniform(0.5, 1.5, size=384).astype(np.float32)
     x0 = f16(rng.normal(size=(rows, 384)))
     x = upf(eng, x0)
-    run(eng, K_RESID, [rows, kdim], [upf(eng, a), up(eng, w), up(eng, b), up(eng, ls), x])
+    run(eng, K_RESID, [rows, kdim], [upf(eng, a), upf(eng, w), up(eng, b), up(eng, ls), x])
     y = readf(eng, x, rows, 384)
     ref = x0.astype(np.float64) + ls * oracle.linear(a.astype(np.float64), w.astype(np.float64), b)
     check(y, ref, atol=2e-3, what=f"resid rows={rows} k={kdim}")
@@ -303,7 +303,7 @@ def test_swiglu(eng, rows):
     bg, bu = (rng.normal(size=1536) * 0.2).astype(np.float32), (rng.normal(size=1536) * 0.2).astype(np.float32)
     w, b = pack_gateup(wg, wu, bg, bu)
     act = allocf(eng, rows, 1536)
-    run(eng, K_SWIGLU, [rows], [upf(eng, h), up(eng, w), up(eng, b), act])
+    run(eng, K_SWIGLU, [rows], [upf(eng, h), upf(eng, w), up(eng, b), act])
     y = readf(eng, act, rows, 1536)
     hd = h.astype(np.float64)
     ref = oracle.swiglu(oracle.linear(hd, wg.astype(np.float64), bg), oracle.linear(hd, wu.astype(np.float64), bu))
@@ -320,7 +320,7 @@ def test_splitk_and_reduce(eng, rows):
     ls = rng.uniform(0.5, 1.5, size=384).astype(np.float32)
     x0 = f16(rng.normal(size=(rows, 384)))
     part = eng.allocate(splits * rows * 384 * 4)
-    run(eng, K_SPLITK, [rows, kdim, splits], [upf(eng, a), up(eng, w), part])
+    run(eng, K_SPLITK, [rows, kdim, splits], [upf(eng, a), upf(eng, w), part])
     p = eng.read(part, np.float32, (splits, rows, 384))
     ad, wd = a.astype(np.float64), w.astype(np.float64)
     c = kdim // splits
@@ -349,6 +349,11 @@ def test_launch_validation_happens_before_any_launch(eng):
         eng.record(next(_keys), [(K_LN, [10], [big, g])])
     with pytest.raises(d.DINOv3Error, match="tpad"):
         eng.record(next(_keys), [(K_ATTN, [1, 14, 200], [big, big, big, big])])
+    # The GEMM K loops run six 64-deep stages per iteration.
+    with pytest.raises(d.DINOv3Error, match="multiple of 384"):
+        eng.record(next(_keys), [(K_RESID, [32, 128], [big, big, g, g, big])])
+    with pytest.raises(d.DINOv3Error, match="multiples of 384"):
+        eng.record(next(_keys), [(K_SPLITK, [32, 768, 4], [big, big, big])])
     with pytest.raises(d.DINOv3Error, match="not been prepared"):
         eng.replay(987654321)
 
@@ -389,7 +394,7 @@ def test_resid_stats(eng, rows, kdim):
     ls = rng.uniform(0.5, 1.5, size=384).astype(np.float32)
     x0 = f16(rng.normal(size=(rows, 384)) * 2 + 0.7)
     x, st = upf(eng, x0), eng.allocate(rows * 48)
-    run(eng, K_RESID_S, [rows, kdim], [upf(eng, a), up(eng, w), up(eng, b), up(eng, ls), x, st])
+    run(eng, K_RESID_S, [rows, kdim], [upf(eng, a), upf(eng, w), up(eng, b), up(eng, ls), x, st])
     y = readf(eng, x, rows, 384)
     ref = x0.astype(np.float64) + ls * oracle.linear(a.astype(np.float64), w.astype(np.float64), b)
     check(y, ref, atol=2e-3, what=f"resid+stats rows={rows} k={kdim}")
@@ -468,7 +473,7 @@ def test_swiglu_layernorm_fused(eng, rows, offset):
     w, b = pack_gateup(wg, wu, bg, bu)
     wl, wsum, t = fold(w, b, gamma, beta)
     act = allocf(eng, rows, 1536)
-    run(eng, K_SWIGLU_LN, [rows], [upf(eng, x), up(eng, slot_stats(x)), up(eng, wl), up(eng, wsum), up(eng, t), act])
+    run(eng, K_SWIGLU_LN, [rows], [upf(eng, x), up(eng, slot_stats(x)), upf(eng, wl), up(eng, wsum), up(eng, t), act])
     y = readf(eng, act, rows, 1536)
     h = oracle.layernorm(x.astype(np.float64), gamma, beta)
     ref = oracle.swiglu(oracle.linear(h, wg.astype(np.float64), bg), oracle.linear(h, wu.astype(np.float64), bu))
