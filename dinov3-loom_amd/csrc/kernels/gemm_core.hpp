@@ -368,61 +368,73 @@ __device__ __forceinline__ void gemm_tile(AL (&al)[P], WL (&wl)[P], int n_tiles,
 
 // Waits until at most N of this wave's vector-memory operations are
 // outstanding and its LDS traffic is done, then joins the workgroup barrier.
-// Vector-memory operations complete in issue order, LDS DMA included.
 template <int N>
 __device__ __forceinline__ void vm_barrier() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
+// Keeps the compiler from moving memory accesses across this point.
+__device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
+
+// Waiting for LDS DMA. Measured on the MI355X: a DMA load can land in LDS
+// after vector loads issued later have completed, so "at most N outstanding"
+// does not prove that a DMA issued before N register loads has landed (a
+// two-buffer loop that relied on it returned different results from launch
+// to launch). DMA loads do complete in issue order among themselves. A wait
+// for DMA stage X is therefore "at most N outstanding" only where every one
+// of the N may be a DMA load issued after X: all register loads are issued
+// before the DMA loads they are waited with.
+
 // The K loop with activations in registers (two sets, ActFrags) and the
-// weight stages moved into three LDS buffers by DMA (WeightDma). At step s
-// the DMA of stage s+2 goes into the buffer that held stage s-1 (read by
-// every wave before the previous barrier), stage s is computed from its
-// buffer, and register set s%2 is refilled with stage s+2. The barrier that
-// ends step s waits for everything but this step's own loads, so stage s+1
-// has landed in LDS for every wave. The three buffers are separate LDS
+// weight stages moved into three LDS buffers by DMA (WeightDma). Step s
+// issues the activation loads of stage s+1 into the register set that held
+// stage s-1, then the DMA of stage s+2 into the buffer that held stage s-1
+// (both released by the previous barrier), computes stage s, and ends with a
+// barrier that waits until only the DMA of stage s+2 may be outstanding:
+// by DMA order stage s+1 has then landed for every wave. Activations get
+// one step to arrive, weights two. The three buffers are separate LDS
 // variables and the loop is unrolled over them, so the compiler can tell a
 // buffer being read from the ones being filled and does not wait for the
-// DMA in flight. DMA stops at the last stage (nothing lands in LDS after
-// the loop); activation loads past it repeat the last stage. k_tiles must be
-// a multiple of 6 (the launchers check).
+// DMA in flight. Nothing is loaded past the last stage. k_tiles must be a
+// multiple of 6 (the launchers check).
 template <class T, class AL, class WD, class Settle>
 __device__ __forceinline__ void gemm_main_dma(AL (&al)[2], const WD& wd, half_t* b0, half_t* b1, half_t* b2, int m0,
                                               int n0, int k_tiles, Acc<T>& acc, Settle&& settle) {
     static_assert(AL::kInRegs, "activations in registers");
-    constexpr int NA = T::FM * (T::BK / 16), NW = WD::PER_WAVE;
-    const int tid = threadIdx.x, last = k_tiles - 1;
+    constexpr int NW = WD::PER_WAVE;
+    const int tid = threadIdx.x;
 #pragma unroll
     for (int i = 0; i < T::FN; ++i)
 #pragma unroll
         for (int j = 0; j < T::FM; ++j) acc.v[i][j] = float16_t{};
     al[0].load(m0, n0, 0, tid);
+    compiler_fence();
     wd.load(b0, n0, 0, tid);
-    al[1].load(m0, n0, min(1, last), tid);
-    if (k_tiles > 1) wd.load(b1, n0, 1, tid);
+    if (k_tiles > 1) wd.load(b1, n0, 1, tid);  // uniform
     settle();
     if (k_tiles > 1)
-        vm_barrier<NA + NW>();
+        vm_barrier<NW>();
     else
-        vm_barrier<NA>();
-    auto step = [&](const half_t* cur, half_t* fill, AL& a, int s) {
+        vm_barrier<0>();
+    auto step = [&](const half_t* cur, half_t* fill, AL& a, AL& next, int s) {
         const bool more = s + 2 < k_tiles;  // uniform
+        if (s + 1 < k_tiles) next.load(m0, n0, s + 1, tid);
+        compiler_fence();
         if (more) wd.load(fill, n0, s + 2, tid);
         mma_stage_frag<T>(cur, tid, a, acc);
-        a.load(m0, n0, min(s + 2, last), tid);
         if (more)
-            vm_barrier<NA + NW>();
-        else
-            vm_barrier<NA>();
+            vm_barrier<NW>();
+        else if (s + 1 < k_tiles)
+            vm_barrier<0>();
     };
     for (int kt = 0; kt < k_tiles; kt += 6) {
-        step(b0, b2, al[0], kt);
-        step(b1, b0, al[1], kt + 1);
-        step(b2, b1, al[0], kt + 2);
-        step(b0, b2, al[1], kt + 3);
-        step(b1, b0, al[0], kt + 4);
-        step(b2, b1, al[1], kt + 5);
+        step(b0, b2, al[0], al[1], kt);
+        step(b1, b0, al[1], al[0], kt + 1);
+        step(b2, b1, al[0], al[1], kt + 2);
+        step(b0, b2, al[1], al[0], kt + 3);
+        step(b1, b0, al[0], al[1], kt + 4);
+        step(b2, b1, al[1], al[0], kt + 5);
     }
 }
 

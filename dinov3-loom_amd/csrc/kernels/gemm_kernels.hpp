@@ -143,15 +143,13 @@ __device__ __forceinline__ void init_frags(ActFrags<T> (&al)[2], const half_t* a
 // partner c+32 of a head are acc.v[2h] / acc.v[2h+1] of the same lane, and
 // both use angle column c of the RoPE tables (DINOv3's tables repeat columns
 // 0..31 in 32..63; only the first half is read). Results are rounded to f16
-// into a per-wave LDS block, then written as whole 128-byte head rows:
-// q, k and v are all head-major [image][head][tpad][64], and the rows of one
-// image are contiguous there.
+// and regrouped in registers (frag_swap) so each lane holds 8 consecutive
+// channels of its row, written as 16-byte pieces of the head rows: q, k and
+// v are all head-major [image][head][tpad][64].
 template <class T, bool LN>
 __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void qkv_rope_kernel(QkvArgs p) {
     static_assert(T::TN == 2 * kHeadDim && T::WGN == 1, "two heads per wave, whole rows per wave");
-    constexpr int SP = T::TN + 8;  // staging pitch in halfs
-    constexpr int LDS = T::WAVES * T::TM * SP > 2 * T::W_HALFS ? T::WAVES * T::TM * SP : 2 * T::W_HALFS;
-    __shared__ __attribute__((aligned(16))) half_t lds[LDS];
+    __shared__ __attribute__((aligned(16))) half_t wb0[T::WF_HALFS], wb1[T::WF_HALFS], wb2[T::WF_HALFS];
     __shared__ __attribute__((aligned(16))) float cst[2][T::BN];  // bias, wsum of the tile's columns
     __shared__ float2_t rows_norm[T::BM];                          // (mean, rstd) of the tile's rows
     static_assert(T::BN <= T::THREADS, "one thread per column constant");
@@ -160,13 +158,13 @@ __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void qkv_rope_kerne
     const int tid = threadIdx.x;
     ActFrags<T> al[2];
     init_frags(al, p.h, M, kHidden);
-    WeightRows<T> wl[2] = {{{}, p.w, kHidden, 0}, {{}, p.w, kHidden, 0}};
+    WeightDma<T> wd(p.w, 3 * kHidden, kHidden);
     // The epilogue's own operands are loaded ahead of the K loop and wait in
     // LDS: the tile's column constants and its rows' LayerNorm (mean, rstd).
     float4_t raw[T::FM][3];
     float cb = 0.f, cw = 0.f;
-    gemm_tile<T>(
-        al, wl, NT, NT * ((M + T::BM - 1) / T::BM), kHidden / T::BK, lds,
+    gemm_tile_dma<T>(
+        al, wd, wb0, wb1, wb2, NT, NT * ((M + T::BM - 1) / T::BM), kHidden / T::BK,
         [&](int m0, int n0) {
             const Frag<T> f(m0, n0);
             if constexpr (LN) {
@@ -199,13 +197,13 @@ __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void qkv_rope_kerne
         },
         [&](const Acc<T>& acc, int m0, int n0) {
         const Frag<T> f(m0, n0);
-        const int lane = threadIdx.x & 63;
-        half_t* const st = lds + (threadIdx.x >> 6) * (T::TM * SP);
         const int part = f.n_base / kHidden, head0 = (f.n_base % kHidden) / kHeadDim;
+        half_t* const out = part == 0 ? p.q : part == 1 ? p.k : p.v;
 #pragma unroll
         for (int j = 0; j < T::FM; ++j) {
-            const int m = min(f.row(j), M - 1);  // rows past M are computed but never written out
-            const int tok = m % Tok;
+            const int mr = f.row(j);
+            const int m = min(mr, M - 1);  // rows past M are computed but never written out
+            const int img = m / Tok, tok = m - img * Tok;
             // RoPE angles of this row, gathered together before any use (lanes
             // hold different rows); prefix rows and v rotate by cos 1, sin 0.
             const size_t angle_row = (size_t)max(tok - kPrefix, 0) * kHeadDim;
@@ -226,14 +224,14 @@ __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void qkv_rope_kerne
                     si[g] = float4_t{};
                 }
             }
-            half_t* const srow = st + (j * 32 + f.l32) * SP;
             RowNorm rn{0.f, 1.f};
             if constexpr (LN) {
                 const float2_t v = rows_norm[f.m_base - m0 + j * 32 + f.l32];
                 rn = RowNorm{v[0], v[1]};
             }
 #pragma unroll
-            for (int h2 = 0; h2 < 2; ++h2)
+            for (int h2 = 0; h2 < 2; ++h2) {
+                half4_t lo_h[4], up_h[4];
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const int c = g * 8 + f.hi * 4;  // channel in the head (0..31); partner c + 32
@@ -245,31 +243,19 @@ __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void qkv_rope_kerne
                     }
                     lo += *(const float4_t*)&cst[0][nl];
                     up += *(const float4_t*)&cst[0][nl + 32];
-                    const float4_t nlo = lo * co[g] - up * si[g];  // x[c] cos - x[c+32] sin
-                    const float4_t nup = up * co[g] + lo * si[g];  // x[c+32] cos + x[c] sin
-                    *(half4_t*)(srow + h2 * kHeadDim + c) = to_half4(nlo);
-                    *(half4_t*)(srow + h2 * kHeadDim + 32 + c) = to_half4(nup);
+                    lo_h[g] = to_half4(lo * co[g] - up * si[g]);  // x[c] cos - x[c+32] sin
+                    up_h[g] = to_half4(up * co[g] + lo * si[g]);  // x[c+32] cos + x[c] sin
                 }
-        }
-        wave_lds_sync();
-        // Copy-out: 8 lanes per 128-byte head row, 8 rows per pass.
-        half_t* const out = part == 0 ? p.q : part == 1 ? p.k : p.v;
-        const int r0 = lane >> 3, ch = (lane & 7) * 8;
-        int mr = f.m_base + r0;
-        int img = mr / Tok, t = mr - img * Tok;
-#pragma unroll
-        for (int it = 0; it < T::TM / 8; ++it) {
-            if (mr < M) {
-#pragma unroll
-                for (int h2 = 0; h2 < 2; ++h2)
-                    *(half8_t*)(out + (((size_t)img * kHeads + head0 + h2) * p.tpad + t) * kHeadDim + ch) =
-                        *(const half8_t*)(st + (it * 8 + r0) * SP + h2 * kHeadDim + ch);
-            }
-            mr += 8;
-            t += 8;
-            while (t >= Tok) {
-                t -= Tok;
-                ++img;
+                // Channels 16kk + 8hi .. +7 of the head for kk = 0..3.
+                const half8_t c0 = frag_swap(lo_h[0], lo_h[1]), c1 = frag_swap(lo_h[2], lo_h[3]);
+                const half8_t c2 = frag_swap(up_h[0], up_h[1]), c3 = frag_swap(up_h[2], up_h[3]);
+                half_t* const row = out + (((size_t)img * kHeads + head0 + h2) * p.tpad + tok) * kHeadDim + f.hi * 8;
+                if (mr < M) {
+                    *(half8_t*)(row) = c0;
+                    *(half8_t*)(row + 16) = c1;
+                    *(half8_t*)(row + 32) = c2;
+                    *(half8_t*)(row + 48) = c3;
+                }
             }
         }
     });

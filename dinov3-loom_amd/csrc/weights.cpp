@@ -185,12 +185,12 @@ Packed load_weights(const std::string& path, uint32_t grid) {
                 qb.insert(qb.end(), b.begin(), b.end());
             }
         }
-        emit(l + "qkv_w", qw, true);
+        out.emplace_back(l + "qkv_w", fragment_order(pack_f16(l + "qkv_w", qw.data(), qw.size()), 1152, 384));
         emit(l + "qkv_b", qb, false);
         {
             Folded f = fold_layernorm(l + "qkv_wln", qw, qb, get(st, p + "norm1.weight", {384}),
                                       get(st, p + "norm1.bias", {384}), 1152, 384);
-            out.emplace_back(l + "qkv_wln", std::move(f.w));
+            out.emplace_back(l + "qkv_wln", fragment_order(f.w, 1152, 384));
             emit(l + "qkv_wsum", f.wsum, false);
             emit(l + "qkv_t", f.t, false);
         }

@@ -21,7 +21,7 @@ std::vector<uint8_t> pack_f16(const std::string& name, const float* values, size
 // qkv_t, gateup_w, gateup_b, gateup_wln, gateup_wsum, gateup_t, o_w, o_b,
 // down_w, down_b}, norm_w, norm_b, rope_cos, rope_sin. gateup_* rows are
 // interleaved in blocks of 32 gate rows then the 32 matching up rows;
-// gateup_w, gateup_wln, o_w and down_w are in fragment order (32-row x
+// qkv_w, qkv_wln, gateup_w, gateup_wln, o_w and down_w are in fragment order (32-row x
 // 16-column blocks, as the GEMMs' weight DMA reads them). The
 // *_wln / *_wsum / *_t tensors fold the preceding LayerNorm into the GEMM
 // (see DHX_K_QKV_ROPE_LN in dinov3_engine.h).

@@ -65,10 +65,10 @@ typedef struct dhx_region {
  * ((k8/8)%2*32 + m%32)*8 — each 32-row x 16-column block is the 1 KB operand
  * a wave feeds one v_mfma_f32_32x32x16_f16, so GEMMs load activations straight
  * into registers. Binding sizes count the padded rows. dhx_fragment_order and
- * dhx_row_order convert on the host. The weights of the residual, SwiGLU and
- * split-K GEMMs (w [384][k], gateup_w, gateup_wln) are in the same fragment
- * order (their row counts are multiples of 32): the kernels move them into
- * LDS block by block with DMA loads.
+ * dhx_row_order convert on the host. The weights of the QKV, residual, SwiGLU
+ * and split-K GEMMs (qkv_w, qkv_wln, w [384][k], gateup_w, gateup_wln) are in
+ * the same fragment order (their row counts are multiples of 32): the kernels
+ * move them into LDS block by block with DMA loads.
  * q, k and v are [images][6][tpad][64] f16 (rows T .. tpad-1 are never
  * written and must hold finite values for attention: regions from
  * dhx_allocate start zeroed), tpad a multiple of 128 >= T = grid*grid + 5;

@@ -231,7 +231,7 @@ def test_qkv_rope(eng, images, grid):
     sin[:, 32:] = np.nan
     nb = images * 6 * tpad * 64 * 2
     q, k, v = eng.allocate(nb), eng.allocate(nb), eng.allocate(nb)
-    run(eng, K_QKV, [images, grid, tpad], [upf(eng, h), up(eng, w), up(eng, b), up(eng, cos), up(eng, sin), q, k, v])
+    run(eng, K_QKV, [images, grid, tpad], [upf(eng, h), upf(eng, w), up(eng, b), up(eng, cos), up(eng, sin), q, k, v])
     gq = eng.read(q, np.float16, (images, 6, tpad, 64))
     gk = eng.read(k, np.float16, (images, 6, tpad, 64))
     gv = eng.read(v, np.float16, (images, 6, tpad, 64))
@@ -449,7 +449,7 @@ def test_qkv_rope_layernorm_fused(eng, images, grid, offset):
     nb = images * 6 * tpad * 64 * 2
     q, k, v = eng.allocate(nb), eng.allocate(nb), eng.allocate(nb)
     run(eng, K_QKV_LN, [images, grid, tpad],
-        [upf(eng, x), up(eng, slot_stats(x)), up(eng, wl), up(eng, wsum), up(eng, t), up(eng, cos), up(eng, sin),
+        [upf(eng, x), up(eng, slot_stats(x)), upf(eng, wl), up(eng, wsum), up(eng, t), up(eng, cos), up(eng, sin),
          q, k, v])
     gq = eng.read(q, np.float16, (images, 6, tpad, 64))
     gv = eng.read(v, np.float16, (images, 6, tpad, 64))
@@ -478,3 +478,63 @@ def test_swiglu_layernorm_fused(eng, rows, offset):
     h = oracle.layernorm(x.astype(np.float64), gamma, beta)
     ref = oracle.swiglu(oracle.linear(h, wg.astype(np.float64), bg), oracle.linear(h, wu.astype(np.float64), bu))
     check(y, ref, atol=3e-3, what=f"fused-LN swiglu rows={rows}")
+
+
+# ---------------------------------------------------------------------------
+# Bitwise repeatability of the GEMM kernels at the batch-64 shapes. The GEMMs
+# move their weight stages into LDS with DMA loads; waiting for one correctly
+# depends on the order in which those loads and the register loads complete,
+# and a wrong wait shows up as results that change from launch to launch
+# (stale weights in LDS), not as a fault.
+
+@pytest.mark.parametrize("kernel", ["qkv_ln", "swiglu_ln", "resid_384", "resid_1536", "splitk"])
+def test_gemm_bitwise_repeatable(eng, kernel):
+    rng = np.random.default_rng(5)
+    images, grid = 64, 14
+    T = grid * grid + 5
+    tpad = (T + 127) // 128 * 128
+    M = images * T
+    x = f16(rng.normal(size=(M, 384)))
+    if kernel == "qkv_ln":
+        w = f16(rng.normal(size=(1152, 384)) * 0.05)
+        cos, sin = oracle.rope_tables(grid)
+        binds = [upf(eng, x), up(eng, slot_stats(x)), upf(eng, w), up(eng, w.astype(np.float64).sum(1).astype(np.float32)),
+                 up(eng, (rng.normal(size=1152) * 0.1).astype(np.float32)), up(eng, cos), up(eng, sin)]
+        nb = images * 6 * tpad * 64 * 2
+
+        def once():
+            out = [eng.allocate(nb) for _ in range(3)]
+            run(eng, K_QKV_LN, [images, grid, tpad], binds + out)
+            return np.concatenate([eng.read(r, np.float16, (nb // 2,)) for r in out])
+    elif kernel == "swiglu_ln":
+        w = f16(rng.normal(size=(3072, 384)) * 0.05)
+        binds = [upf(eng, x), up(eng, slot_stats(x)), upf(eng, w), up(eng, w.astype(np.float64).sum(1).astype(np.float32)),
+                 up(eng, (rng.normal(size=3072) * 0.1).astype(np.float32))]
+
+        def once():
+            act = allocf(eng, M, 1536)
+            run(eng, K_SWIGLU_LN, [M], binds + [act])
+            return readf(eng, act, M, 1536)
+    else:
+        kd = 384 if kernel == "resid_384" else 1536
+        a = f16(rng.normal(size=(M, kd)))
+        w = f16(rng.normal(size=(384, kd)) * 0.03)
+        binds = [upf(eng, a), upf(eng, w)]
+        if kernel == "splitk":
+            def once():
+                part = eng.allocate(4 * M * 384 * 4)
+                run(eng, K_SPLITK, [M, kd, 4], binds + [part])
+                return eng.read(part, np.float32, (4 * M * 384,))
+        else:
+            consts = [up(eng, (rng.normal(size=384) * 0.1).astype(np.float32)), up(eng, np.ones(384, np.float32))]
+
+            def once():
+                xr, st = upf(eng, x), eng.allocate(M * 48)
+                run(eng, K_RESID_S, [M, kd], binds + consts + [xr, st])
+                return np.concatenate([readf(eng, xr, M, 384).astype(np.float32).ravel(),
+                                       eng.read(st, np.float32, (M * 12,))])
+    first = once()
+    assert np.all(np.isfinite(first))
+    for rep in range(4):
+        again = once()
+        assert np.array_equal(first, again), f"{kernel}: launch {rep + 2} differs in {int((first != again).sum())} elements"
