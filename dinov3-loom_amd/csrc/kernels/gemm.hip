@@ -16,6 +16,7 @@ using gemm::tiles_for;
 using PatchTile = Tile<64, 128, 2, 2>;
 using QkvTile = Tile<128, 128, 4, 1>;
 using ResidTile = Tile<128, 64, 4, 1>;
+using ResidTileK = Tile<128, 64, 4, 1, 128>;  // down projection (k = 1536)
 using SwigluTile = Tile<256, 128, 4, 1, 32>;
 using SplitTile = Tile<128, 128, 4, 1>;
 
@@ -42,6 +43,11 @@ hipError_t launch_qkv_rope(const QkvArgs& a, hipStream_t s) {
 hipError_t launch_resid(const ResidArgs& a, hipStream_t s) {
     // The K loop walks its stages six at a time (gemm_main_dma).
     if (a.k % (6 * ResidTile::BK) != 0) return hipErrorInvalidValue;
+    if (a.k % (6 * ResidTileK::BK) == 0) {
+        const int tiles = tiles_for<ResidTileK>(a.rows, kHidden);
+        return a.stats ? launch<ResidTileK>(gemm::resid_kernel<ResidTileK, true>, tiles, a, s)
+                       : launch<ResidTileK>(gemm::resid_kernel<ResidTileK, false>, tiles, a, s);
+    }
     const int tiles = tiles_for<ResidTile>(a.rows, kHidden);
     return a.stats ? launch<ResidTile>(gemm::resid_kernel<ResidTile, true>, tiles, a, s)
                    : launch<ResidTile>(gemm::resid_kernel<ResidTile, false>, tiles, a, s);

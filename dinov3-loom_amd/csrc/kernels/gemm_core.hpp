@@ -32,7 +32,7 @@ struct Tile {
     // LDS row pitch in halfs (144 B for BK 64, 80 B for BK 32): the 16-byte
     // fragment reads of 8 consecutive rows hit disjoint banks.
     static constexpr int LDK = BK + 8;
-    static_assert(BK == 64 || BK == 32, "stage depth");
+    static_assert(BK == 128 || BK == 64 || BK == 32, "stage depth");
     static constexpr int WAVES = WGM * WGN, THREADS = 64 * WAVES;
     static constexpr int TM = BM / WGM, TN = BN / WGN;
     static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile is a multiple of the 32x32 MFMA tile");

@@ -268,7 +268,7 @@ __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void qkv_rope_kerne
 // fragment (1 KB contiguous per wave access); LDS holds only the weight
 // stages and the column constants.
 template <class T, bool STATS>
-__global__ __launch_bounds__(T::THREADS, 4) void resid_kernel(ResidArgs p) {
+__global__ __launch_bounds__(T::THREADS, T::BK == 128 ? 3 : 4) void resid_kernel(ResidArgs p) {
     static_assert(T::TN % 64 == 0 && T::TM == 32, "whole statistics slots, one 32-row block per wave");
     static_assert(T::BN <= T::THREADS, "one thread per column constant");
     constexpr int XF = T::TN / 16;  // x fragments per wave
