@@ -3,8 +3,12 @@
 //
 // One workgroup = 4 waves = 128 queries of one (image, head); each wave owns
 // 32 queries. Keys stream through LDS in blocks of 64 (K and V both as
-// [key][ch], double-buffered), so the same kernel serves 201 tokens
-// (224x224) and 1029 tokens (512x512).
+// [key][ch]), so the same kernel serves 201 tokens (224x224) and 1029
+// tokens (512x512). The blocks move from global memory straight into three
+// LDS buffers with DMA loads (buffer_load ... lds), two blocks ahead; each
+// 128-byte key row is stored with its 16-byte chunks XOR-swizzled by the
+// row (chunk c of row r at slot c ^ (r % 8)), so the row reads of K and the
+// transpose reads of V hit distinct banks.
 //
 // Everything is computed transposed so that a lane owns one query:
 //   S^T = K . Q^T      (MFMA a = K rows from LDS, b = Q^T held in registers)
@@ -25,19 +29,30 @@ namespace dhx {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int KB = 64;    // keys per LDS block
-constexpr int KLD = 72;   // LDS row pitch in halfs
-constexpr int QB = 128;   // queries per workgroup
-constexpr float kLazy = 8.0f;  // running-max slack of the lazy rescaling (score units)
+constexpr int KB = 64;                   // keys per LDS block
+constexpr int BLK = KB * kHeadDim;       // halfs per K (or V) block
+constexpr int QB = 128;                  // queries per workgroup
+constexpr float kLazy = 8.0f;            // running-max slack of the lazy rescaling (score units)
 
 __device__ __forceinline__ half8_t zero8() {
     half8_t z = {};
     return z;
 }
 
+// Element offset of channel ch (a multiple of 4) of key row r inside a
+// swizzled block.
+__device__ __forceinline__ int swz(int r, int ch) { return r * kHeadDim + ((((ch >> 3) ^ r) & 7) << 3) + (ch & 7); }
+
+// Waits until at most N of this wave's vector-memory operations are
+// outstanding and its LDS traffic is done, then joins the workgroup barrier.
+template <int N>
+__device__ __forceinline__ void vm_barrier() {
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
 __global__ __launch_bounds__(kThreads, 3) void attention_kernel(AttentionArgs p) {
-    __shared__ half_t sK[2][KB * KLD];
-    __shared__ half_t sV[2][KB * KLD];
+    __shared__ __attribute__((aligned(16))) half_t sK0[BLK], sK1[BLK], sK2[BLK];
+    __shared__ __attribute__((aligned(16))) half_t sV0[BLK], sV1[BLK], sV2[BLK];
     // 1-D grid, XCD-aware: the tile space (query block fastest, then head,
     // then image) is cut into 8 contiguous chunks, one per XCD, so the query
     // blocks of one (image, head) share K and V in that XCD's L2.
@@ -45,43 +60,50 @@ __global__ __launch_bounds__(kThreads, 3) void attention_kernel(AttentionArgs p)
     const int per = (total + 7) >> 3, g = blockIdx.x, t = (g & 7) * per + (g >> 3);
     if ((g >> 3) >= per || t >= total) return;  // uniform per workgroup
     const int qb = t % nqb, head = (t / nqb) % kHeads, img = t / (nqb * kHeads);
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l32 = lane & 31, hi = lane >> 5;
     const int T = p.tokens;
     const size_t bh = (size_t)img * kHeads + head;
     const half_t* qg = p.q + bh * p.tpad * kHeadDim;
-    const half_t* kg = p.k + bh * p.tpad * kHeadDim;
-    const half_t* vg = p.v + bh * p.tpad * kHeadDim;
+    const int nkb = (T + KB - 1) / KB;  // nkb * KB <= tpad, so every block row exists
 
-    const int nkb = (T + KB - 1) / KB;
+    // Block kb of K and V: wave w moves key rows 16w .. 16w+15 of each, as
+    // two 1 KB DMA loads per matrix (8 rows each). Lane i lands at LDS slot
+    // (row i/8, chunk slot i%8) and fetches the chunk the swizzle puts there.
+    const uint32_t bytes = (uint32_t)p.tpad * kHeadDim * 2;
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<half_t*>(p.k + bh * p.tpad * kHeadDim), 0, bytes, kBufferRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<half_t*>(p.v + bh * p.tpad * kHeadDim), 0, bytes, kBufferRsrcWord3);
+    const int voff = (lane >> 3) * 128 + (((lane & 7) ^ (lane >> 3)) << 4);
+    auto dma = [&](half_t* k_buf, half_t* v_buf, int kb) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int row = wave * 16 + j * 8, soff = (kb * KB + row) * 128;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(k_buf + row * kHeadDim),
+                                                     16, voff, soff, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)(v_buf + row * kHeadDim),
+                                                     16, voff, soff, 0, 0);
+        }
+    };
+    constexpr int kDmaPerBlock = 4;  // per wave
+
+    // Block 0 first, then the Q fragments (registers), then block 1: the
+    // wait for block 0 counts only the DMA loads of block 1 (DMA loads land
+    // in issue order among themselves, but not in order with register loads).
+    dma(sK0, sV0, 0);
     const int qrow = qb * QB + wave * 32 + l32;
     half8_t qf[4];
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
         qf[kk] = qrow < T ? *(const half8_t*)(qg + (size_t)qrow * kHeadDim + kk * 16 + hi * 8) : zero8();
-
-    // Each thread moves two 16-byte pieces of the K block and two of V. Two
-    // register sets: the loads of block kb+2 are issued while block kb is
-    // computed, so each has two blocks of compute to land (a block is short
-    // next to an L2 round trip). Loads past the last block repeat it.
-    half8_t kr[2][2], vr[2][2];
-    auto load = [&](int set, int kb) {
-        kb = min(kb, nkb - 1);
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int c = tid + i * kThreads, row = c >> 3, col = (c & 7) * 8;
-            kr[set][i] = *(const half8_t*)(kg + (size_t)(kb * KB + row) * kHeadDim + col);
-            vr[set][i] = *(const half8_t*)(vg + (size_t)(kb * KB + row) * kHeadDim + col);
-        }
-    };
-    auto store = [&](int set, int buf) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int c = tid + i * kThreads, row = c >> 3, col = (c & 7) * 8;
-            *(half8_t*)(&sK[buf][row * KLD + col]) = kr[set][i];
-            *(half8_t*)(&sV[buf][row * KLD + col]) = vr[set][i];
-        }
-    };
+    asm volatile("" ::: "memory");
+    if (nkb > 1) {
+        dma(sK1, sV1, 1);
+        vm_barrier<kDmaPerBlock>();
+    } else {
+        vm_barrier<0>();
+    }
 
     // Transpose-read position of this lane inside a 4-key x 32-channel patch
     // of the V block: lane j of each 16-lane group then receives channel
@@ -99,27 +121,24 @@ __global__ __launch_bounds__(kThreads, 3) void attention_kernel(AttentionArgs p)
     // Waves whose 32 queries all lie past T only help move K and V.
     const bool active = qb * QB + wave * 32 < T;
 
-    load(0, 0);
-    load(1, 1);
-    store(0, 0);
-    lds_barrier();
-    auto block = [&](int kb, int buf) {
+    auto block = [&](const half_t* sK, const half_t* sV, int kb) {
 #pragma unroll
         for (int sub = 0; sub < 2 && active; ++sub) {
             const int key0 = kb * KB + sub * 32;
             if (key0 >= T) break;  // uniform across the workgroup
             float16_t s = {};
-            const half_t* krow = &sK[buf][(sub * 32 + l32) * KLD + hi * 8];
-    #pragma unroll
-            for (int kk = 0; kk < 4; ++kk) s = mfma32x32x16(*(const half8_t*)(krow + kk * 16), qf[kk], s);
+            const int kr = sub * 32 + l32;
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk)
+                s = mfma32x32x16(*(const half8_t*)(sK + swz(kr, kk * 16 + hi * 8)), qf[kk], s);
             // s[r] is the score of key key0 + 8(r/4) + 4*hi + r%4 for query l32.
             if (key0 + 32 > T) {  // the last, partial block of keys (uniform)
-    #pragma unroll
+#pragma unroll
                 for (int r = 0; r < 16; ++r)
                     if (key0 + 8 * (r >> 2) + 4 * hi + (r & 3) >= T) s[r] = neg_inf;
             }
             float mx = s[0];
-    #pragma unroll
+#pragma unroll
             for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
             mx = half_pair_max(mx);  // every sub-block holds a valid key of each pair
             // Lazy rescaling: the running max moves only when a score exceeds
@@ -136,7 +155,7 @@ __global__ __launch_bounds__(kThreads, 3) void attention_kernel(AttentionArgs p)
             }
             const float mb = m_run * kLog2e;
             float sum = 0.f;
-    #pragma unroll
+#pragma unroll
             for (int r = 0; r < 16; ++r) {
                 s[r] = fast_exp2(fmaf(s[r], kLog2e, -mb));
                 sum += s[r];
@@ -147,47 +166,60 @@ __global__ __launch_bounds__(kThreads, 3) void attention_kernel(AttentionArgs p)
             // key0 + 16ks + (j < 4 ? 4hi + j : 8 + 4hi + j - 4); the V^T
             // transpose reads below give channel ct*32 + l32 of the same keys.
             half8_t pb[2];
-    #pragma unroll
+#pragma unroll
             for (int ks = 0; ks < 2; ++ks)
-    #pragma unroll
+#pragma unroll
                 for (int e = 0; e < 8; ++e) pb[ks][e] = (half_t)s[8 * ks + e];
-    #pragma unroll
+#pragma unroll
             for (int ct = 0; ct < 2; ++ct)
-    #pragma unroll
+#pragma unroll
                 for (int ks = 0; ks < 2; ++ks) {
-                    const half_t* vb = &sV[buf][(sub * 32 + ks * 16 + 4 * hi + tr_row) * KLD + ct * 32 + tr_col];
-                    const half4_t a0 = lds_read_tr16(vb), a1 = lds_read_tr16(vb + 8 * KLD);
+                    const int vr = sub * 32 + ks * 16 + 4 * hi + tr_row;
+                    const half4_t a0 = lds_read_tr16(sV + swz(vr, ct * 32 + tr_col));
+                    const half4_t a1 = lds_read_tr16(sV + swz(vr + 8, ct * 32 + tr_col));
                     const half8_t va = __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7);
                     o[ct] = mfma32x32x16(va, pb[ks], o[ct]);
                 }
         }
     };
-    for (int kb = 0; kb < nkb; kb += 2) {
-        load(0, kb + 2);
-        block(kb, 0);
-        if (kb + 1 < nkb) store(1, 1);
-        lds_barrier();
+    // Block kb is computed from buffer kb % 3 while the DMA of block kb+2
+    // fills the buffer of block kb-1 (released by the previous barrier). The
+    // barrier after block kb waits until only block kb+2's DMA may be in
+    // flight, so block kb+1 has landed for every wave.
+    auto step = [&](const half_t* k_cur, const half_t* v_cur, half_t* k_fill, half_t* v_fill, int kb) {
+        const bool more = kb + 2 < nkb;  // uniform
+        if (more) dma(k_fill, v_fill, kb + 2);
+        block(k_cur, v_cur, kb);
+        if (more)
+            vm_barrier<kDmaPerBlock>();
+        else if (kb + 1 < nkb)
+            vm_barrier<0>();
+    };
+    for (int kb = 0; kb < nkb; kb += 3) {
+        step(sK0, sV0, sK2, sV2, kb);
         if (kb + 1 >= nkb) break;
-        load(1, kb + 3);
-        block(kb + 1, 1);
-        if (kb + 2 < nkb) store(0, 0);
-        lds_barrier();
+        step(sK1, sV1, sK0, sV0, kb + 1);
+        if (kb + 2 >= nkb) break;
+        step(sK2, sV2, sK1, sV1, kb + 2);
     }
 
     if (qrow < T) {
-        // out is in fragment order: the lane's 4 channels are half of one
-        // 8-channel piece of row img*T + qrow (the partner lane l ^ 32 holds
-        // the other half), so the 32 queries of a wave fill whole pieces.
+        // out is in fragment order: each 16-channel half of a 32-channel
+        // block becomes one 8-channel piece per lane after frag_swap.
         const float inv = 1.0f / l_run;
         const int row = img * T + qrow;
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int c = head * kHeadDim + ct * 32 + g * 8 + hi * 4;
-                half4_t v = {(half_t)(o[ct][4 * g] * inv), (half_t)(o[ct][4 * g + 1] * inv),
-                             (half_t)(o[ct][4 * g + 2] * inv), (half_t)(o[ct][4 * g + 3] * inv)};
-                *(half4_t*)(p.out + frag_piece(row, c & ~7, kHidden) + (c & 7)) = v;
+            for (int kk = 0; kk < 2; ++kk) {
+                const float16_t& a = o[ct];
+                const half4_t g0 = {(half_t)(a[8 * kk] * inv), (half_t)(a[8 * kk + 1] * inv),
+                                    (half_t)(a[8 * kk + 2] * inv), (half_t)(a[8 * kk + 3] * inv)};
+                const half4_t g1 = {(half_t)(a[8 * kk + 4] * inv), (half_t)(a[8 * kk + 5] * inv),
+                                    (half_t)(a[8 * kk + 6] * inv), (half_t)(a[8 * kk + 7] * inv)};
+                const half8_t piece = frag_swap(g0, g1);
+                const int c = head * kHeadDim + ct * 32 + kk * 16 + hi * 8;
+                *(half8_t*)(p.out + frag_piece(row, c, kHidden)) = piece;
             }
     }
 }
