@@ -7,8 +7,8 @@
 // tokens (512x512). The blocks move from global memory straight into three
 // LDS buffers with DMA loads (buffer_load ... lds), two blocks ahead; each
 // 128-byte key row is stored with its 16-byte chunks XOR-swizzled by the
-// row (chunk c of row r at slot c ^ (r % 8)), so the row reads of K and the
-// transpose reads of V hit distinct banks.
+// row (swz below), so the row reads of K and the transpose reads of V hit
+// distinct banks.
 //
 // Everything is computed transposed so that a lane owns one query:
 //   S^T = K . Q^T      (MFMA a = K rows from LDS, b = Q^T held in registers)
@@ -39,9 +39,22 @@ __device__ __forceinline__ half8_t zero8() {
     return z;
 }
 
+// LDS on gfx950 has 64 banks of 4 bytes: two 128-byte key rows per bank
+// cycle. Chunk c of key row r sits at slot c ^ swz_slot(r), with
+// swz_slot(r) = f((r / 2) % 8), f(t) = 4 (t % 2) + t / 2 (a bijection). The
+// K row reads of 16 lanes (16 consecutive rows, one chunk) then cover all
+// 64 banks, and so do the V transpose reads (4 consecutive rows x 4 aligned
+// chunks per 32 lanes: rows 2 apart differ in bit 2 of the slot).
+__device__ __forceinline__ int swz_slot(int r) {
+    const int t = (r >> 1) & 7;
+    return ((t & 1) << 2) | (t >> 1);
+}
+
 // Element offset of channel ch (a multiple of 4) of key row r inside a
 // swizzled block.
-__device__ __forceinline__ int swz(int r, int ch) { return r * kHeadDim + ((((ch >> 3) ^ r) & 7) << 3) + (ch & 7); }
+__device__ __forceinline__ int swz(int r, int ch) {
+    return r * kHeadDim + ((((ch >> 3) ^ swz_slot(r)) & 7) << 3) + (ch & 7);
+}
 
 // Waits until at most N of this wave's vector-memory operations are
 // outstanding and its LDS traffic is done, then joins the workgroup barrier.
@@ -75,15 +88,18 @@ __global__ __launch_bounds__(kThreads, 3) void attention_kernel(AttentionArgs p)
         const_cast<half_t*>(p.k + bh * p.tpad * kHeadDim), 0, bytes, kBufferRsrcWord3);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<half_t*>(p.v + bh * p.tpad * kHeadDim), 0, bytes, kBufferRsrcWord3);
-    const int voff = (lane >> 3) * 128 + (((lane & 7) ^ (lane >> 3)) << 4);
+    // Load j covers rows 16w + 8j .. +7 (row % 16 = 8j + lane / 8).
+    int voff[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) voff[j] = (lane >> 3) * 128 + (((lane & 7) ^ swz_slot(j * 8 + (lane >> 3))) << 4);
     auto dma = [&](half_t* k_buf, half_t* v_buf, int kb) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int row = wave * 16 + j * 8, soff = (kb * KB + row) * 128;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(k_buf + row * kHeadDim),
-                                                     16, voff, soff, 0, 0);
+                                                     16, voff[j], soff, 0, 0);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)(v_buf + row * kHeadDim),
-                                                     16, voff, soff, 0, 0);
+                                                     16, voff[j], soff, 0, 0);
         }
     };
     constexpr int kDmaPerBlock = 4;  // per wave
