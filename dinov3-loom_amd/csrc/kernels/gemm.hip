@@ -43,6 +43,16 @@ hipError_t launch_qkv_rope(const QkvArgs& a, hipStream_t s) {
 hipError_t launch_resid(const ResidArgs& a, hipStream_t s) {
     // The K loop walks its stages six at a time (gemm_main_dma).
     if (a.k % (6 * ResidTile::BK) != 0) return hipErrorInvalidValue;
+    if (a.k == kHidden) {  // the o-projection: three 128-deep stages, unrolled
+        const int tiles = tiles_for<ResidTileK>(a.rows, kHidden);
+        return a.stats ? launch<ResidTileK>(gemm::resid_kernel<ResidTileK, true, kHidden / 128>, tiles, a, s)
+                       : launch<ResidTileK>(gemm::resid_kernel<ResidTileK, false, kHidden / 128>, tiles, a, s);
+    }
+    if (a.k == kFF) {  // the down projection: twelve 128-deep stages, unrolled
+        const int tiles = tiles_for<ResidTileK>(a.rows, kHidden);
+        return a.stats ? launch<ResidTileK>(gemm::resid_kernel<ResidTileK, true, kFF / 128>, tiles, a, s)
+                       : launch<ResidTileK>(gemm::resid_kernel<ResidTileK, false, kFF / 128>, tiles, a, s);
+    }
     if (a.k % (6 * ResidTileK::BK) == 0) {
         const int tiles = tiles_for<ResidTileK>(a.rows, kHidden);
         return a.stats ? launch<ResidTileK>(gemm::resid_kernel<ResidTileK, true>, tiles, a, s)
@@ -65,7 +75,10 @@ hipError_t launch_swiglu(const SwigluArgs& a, hipStream_t s) {
 hipError_t launch_splitk(const SplitKArgs& a, hipStream_t s) {
     // Each split's K loop walks its stages six at a time (gemm_main_dma).
     if (a.splits < 1 || a.k % a.splits != 0 || (a.k / a.splits) % (6 * SplitTile::BK) != 0) return hipErrorInvalidValue;
-    return launch<SplitTile>(gemm::splitk_kernel<SplitTile>, tiles_for<SplitTile>(a.rows, kHidden) * a.splits, a, s);
+    const int tiles = tiles_for<SplitTile>(a.rows, kHidden) * a.splits;
+    if (a.k / a.splits == kHidden)  // the model's b = 1 down projection: 4 splits of 384, six stages unrolled
+        return launch<SplitTile>(gemm::splitk_kernel<SplitTile, kHidden / SplitTile::BK>, tiles, a, s);
+    return launch<SplitTile>(gemm::splitk_kernel<SplitTile>, tiles, a, s);
 }
 
 }  // namespace dhx

@@ -396,11 +396,13 @@ __device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory")
 // one step to arrive, weights two. The three buffers are separate LDS
 // variables and the loop is unrolled over them, so the compiler can tell a
 // buffer being read from the ones being filled and does not wait for the
-// DMA in flight. Nothing is loaded past the last stage. k_tiles must be a
-// multiple of 6 (the launchers check).
-template <class T, class AL, class WD, class Settle>
+// DMA in flight. Nothing is loaded past the last stage. With KT > 0 the
+// stage count is KT, known at compile time, and the steps are fully unrolled
+// (any KT); otherwise k_tiles must be a multiple of 6 (the launchers check).
+template <class T, int KT = 0, class AL, class WD, class Settle>
 __device__ __forceinline__ void gemm_main_dma(AL (&al)[2], const WD& wd, half_t* b0, half_t* b1, half_t* b2, int m0,
-                                              int n0, int k_tiles, Acc<T>& acc, Settle&& settle) {
+                                              int n0, int k_tiles_rt, Acc<T>& acc, Settle&& settle) {
+    const int k_tiles = KT > 0 ? KT : k_tiles_rt;
     static_assert(AL::kInRegs, "activations in registers");
     constexpr int NW = WD::PER_WAVE;
     const int tid = threadIdx.x;
@@ -428,18 +430,24 @@ __device__ __forceinline__ void gemm_main_dma(AL (&al)[2], const WD& wd, half_t*
         else if (s + 1 < k_tiles)
             vm_barrier<0>();
     };
-    for (int kt = 0; kt < k_tiles; kt += 6) {
-        step(b0, b2, al[0], al[1], kt);
-        step(b1, b0, al[1], al[0], kt + 1);
-        step(b2, b1, al[0], al[1], kt + 2);
-        step(b0, b2, al[1], al[0], kt + 3);
-        step(b1, b0, al[0], al[1], kt + 4);
-        step(b2, b1, al[1], al[0], kt + 5);
+    if constexpr (KT > 0) {
+        half_t* const bufs[3] = {b0, b1, b2};
+#pragma unroll
+        for (int s = 0; s < KT; ++s) step(bufs[s % 3], bufs[(s + 2) % 3], al[s & 1], al[(s + 1) & 1], s);
+    } else {
+        for (int kt = 0; kt < k_tiles; kt += 6) {
+            step(b0, b2, al[0], al[1], kt);
+            step(b1, b0, al[1], al[0], kt + 1);
+            step(b2, b1, al[0], al[1], kt + 2);
+            step(b0, b2, al[1], al[0], kt + 3);
+            step(b1, b0, al[0], al[1], kt + 4);
+            step(b2, b1, al[1], al[0], kt + 5);
+        }
     }
 }
 
 // gemm_tile over gemm_main_dma.
-template <class T, int NS = 1, class AL, class WD, class Issue, class Settle, class Epi>
+template <class T, int NS = 1, int KT = 0, class AL, class WD, class Issue, class Settle, class Epi>
 __device__ __forceinline__ void gemm_tile_dma(AL (&al)[2], WD& wd, half_t* b0, half_t* b1, half_t* b2, int n_tiles,
                                               int total_tiles, int k_tiles, Issue&& issue, Settle&& settle,
                                               Epi&& epi) {
@@ -448,7 +456,7 @@ __device__ __forceinline__ void gemm_tile_dma(AL (&al)[2], WD& wd, half_t* b0, h
     const int n0 = (t % n_tiles) * T::BN, m0 = (t / n_tiles) * T::BM;
     issue(m0, n0);
     Acc<T> acc;
-    gemm_main_dma<T>(al, wd, b0, b1, b2, m0, n0, k_tiles, acc, settle);
+    gemm_main_dma<T, KT>(al, wd, b0, b1, b2, m0, n0, k_tiles, acc, settle);
     epi(acc, m0, n0);
 }
 

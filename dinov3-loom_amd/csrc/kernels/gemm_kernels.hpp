@@ -163,7 +163,7 @@ __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void qkv_rope_kerne
     // LDS: the tile's column constants and its rows' LayerNorm (mean, rstd).
     float4_t raw[T::FM][3];
     float cb = 0.f, cw = 0.f;
-    gemm_tile_dma<T>(
+    gemm_tile_dma<T, 1, kHidden / T::BK>(
         al, wd, wb0, wb1, wb2, NT, NT * ((M + T::BM - 1) / T::BM), kHidden / T::BK,
         [&](int m0, int n0) {
             const Frag<T> f(m0, n0);
@@ -267,7 +267,7 @@ __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void qkv_rope_kerne
 // fragment in registers (frag_swap) and reads and writes x fragment by
 // fragment (1 KB contiguous per wave access); LDS holds only the weight
 // stages and the column constants.
-template <class T, bool STATS>
+template <class T, bool STATS, int KT = 0>
 __global__ __launch_bounds__(T::THREADS, T::BK == 128 ? 3 : 4) void resid_kernel(ResidArgs p) {
     static_assert(T::TN % 64 == 0 && T::TM == 32, "whole statistics slots, one 32-row block per wave");
     static_assert(T::BN <= T::THREADS, "one thread per column constant");
@@ -290,7 +290,7 @@ __global__ __launch_bounds__(T::THREADS, T::BK == 128 ? 3 : 4) void resid_kernel
         const int mb = min(f.m_base / 32, mblocks - 1);  // a wave past the rows re-reads the last block
         return p.x + ((size_t)mb * (kHidden / 16) + f.n_base / 16 + i) * 512 + lane * 8;
     };
-    gemm_tile_dma<T>(
+    gemm_tile_dma<T, 1, KT>(
         al, wd, wb0, wb1, wb2, NT, NT * ((p.rows + T::BM - 1) / T::BM), p.k / T::BK,
         [&](int m0, int n0) {
 #pragma unroll
@@ -368,7 +368,7 @@ __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void swiglu_kernel(
     float4_t raw[T::FM][3];
     RowNorm rn[T::FM];
     float cb = 0.f, cw = 0.f;
-    gemm_tile_dma<T, kSwigluSlices>(
+    gemm_tile_dma<T, kSwigluSlices, kHidden / T::BK>(
         al, wd, wb0, wb1, wb2, NT, NT * ((p.rows + T::BM - 1) / T::BM), kHidden / T::BK,
         [&](int m0, int n0) {
             const Frag<T> f(m0, n0);
@@ -447,7 +447,7 @@ struct SplitActFrags : ActFrags<T> {
     }
 };
 
-template <class T>
+template <class T, int KT = 0>
 __global__ __launch_bounds__(T::THREADS, 3) void splitk_kernel(SplitKArgs p) {
     __shared__ __attribute__((aligned(16))) half_t wb0[T::WF_HALFS], wb1[T::WF_HALFS], wb2[T::WF_HALFS];
     constexpr int NT = kHidden / T::BN;
@@ -457,7 +457,7 @@ __global__ __launch_bounds__(T::THREADS, 3) void splitk_kernel(SplitKArgs p) {
     init_frags(base, p.a, p.rows, p.k);
     SplitActFrags<T> al[2] = {{base[0], d}, {base[1], d}};
     WeightDma<T> wd(p.w, kHidden, p.k);
-    gemm_tile_dma<T>(
+    gemm_tile_dma<T, 1, KT>(
         al, wd, wb0, wb1, wb2, NT, NT * MT * p.splits, d.kc / T::BK,
         [&](int m0, int) { wd.ks_off = d.split(m0) * (d.kc / 16); }, [] {},
         [&](const Acc<T>& acc, int m0, int n0) {
