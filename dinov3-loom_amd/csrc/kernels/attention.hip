@@ -63,6 +63,10 @@ __device__ __forceinline__ void vm_barrier() {
     asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
+// NKB > 0: the number of key blocks, known at compile time (the block loop is
+// then unrolled, which keeps the compiler's wait counts exact; used for the
+// four blocks of 201 tokens); 0: any.
+template <int NKB>
 __global__ __launch_bounds__(kThreads, 3) void attention_kernel(AttentionArgs p) {
     __shared__ __attribute__((aligned(16))) half_t sK0[BLK], sK1[BLK], sK2[BLK];
     __shared__ __attribute__((aligned(16))) half_t sV0[BLK], sV1[BLK], sV2[BLK];
@@ -78,7 +82,7 @@ __global__ __launch_bounds__(kThreads, 3) void attention_kernel(AttentionArgs p)
     const int T = p.tokens;
     const size_t bh = (size_t)img * kHeads + head;
     const half_t* qg = p.q + bh * p.tpad * kHeadDim;
-    const int nkb = (T + KB - 1) / KB;  // nkb * KB <= tpad, so every block row exists
+    const int nkb = NKB > 0 ? NKB : (T + KB - 1) / KB;  // nkb * KB <= tpad, so every block row exists
 
     // Block kb of K and V: wave w moves key rows 16w .. 16w+15 of each, as
     // two 1 KB DMA loads per matrix (8 rows each). Lane i lands at LDS slot
@@ -108,11 +112,12 @@ __global__ __launch_bounds__(kThreads, 3) void attention_kernel(AttentionArgs p)
     // wait for block 0 counts only the DMA loads of block 1 (DMA loads land
     // in issue order among themselves, but not in order with register loads).
     dma(sK0, sV0, 0);
+    // Queries past T load row T-1 (unconditional loads keep the wait counts
+    // exact); their results are never stored.
     const int qrow = qb * QB + wave * 32 + l32;
     half8_t qf[4];
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
-        qf[kk] = qrow < T ? *(const half8_t*)(qg + (size_t)qrow * kHeadDim + kk * 16 + hi * 8) : zero8();
+    for (int kk = 0; kk < 4; ++kk) qf[kk] = *(const half8_t*)(qg + (size_t)min(qrow, T - 1) * kHeadDim + kk * 16 + hi * 8);
     asm volatile("" ::: "memory");
     if (nkb > 1) {
         dma(sK1, sV1, 1);
@@ -211,12 +216,19 @@ __global__ __launch_bounds__(kThreads, 3) void attention_kernel(AttentionArgs p)
         else if (kb + 1 < nkb)
             vm_barrier<0>();
     };
-    for (int kb = 0; kb < nkb; kb += 3) {
-        step(sK0, sV0, sK2, sV2, kb);
-        if (kb + 1 >= nkb) break;
-        step(sK1, sV1, sK0, sV0, kb + 1);
-        if (kb + 2 >= nkb) break;
-        step(sK2, sV2, sK1, sV1, kb + 2);
+    if constexpr (NKB > 0) {
+        half_t* const kbuf[3] = {sK0, sK1, sK2};
+        half_t* const vbuf[3] = {sV0, sV1, sV2};
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) step(kbuf[kb % 3], vbuf[kb % 3], kbuf[(kb + 2) % 3], vbuf[(kb + 2) % 3], kb);
+    } else {
+        for (int kb = 0; kb < nkb; kb += 3) {
+            step(sK0, sV0, sK2, sV2, kb);
+            if (kb + 1 >= nkb) break;
+            step(sK1, sV1, sK0, sV0, kb + 1);
+            if (kb + 2 >= nkb) break;
+            step(sK2, sV2, sK1, sV1, kb + 2);
+        }
     }
 
     if (qrow < T) {
@@ -244,7 +256,14 @@ __global__ __launch_bounds__(kThreads, 3) void attention_kernel(AttentionArgs p)
 
 hipError_t launch_attention(const AttentionArgs& a, hipStream_t s) {
     const int total = (a.tokens + QB - 1) / QB * kHeads * a.images;
-    hipLaunchKernelGGL(attention_kernel, dim3((total + 7) & ~7), dim3(kThreads), 0, s, a);
+    const dim3 grid((total + 7) & ~7), block(kThreads);
+    switch ((a.tokens + KB - 1) / KB) {
+        case 4:  // 224x224: 201 tokens
+            hipLaunchKernelGGL(attention_kernel<4>, grid, block, 0, s, a);
+            break;
+        default:
+            hipLaunchKernelGGL(attention_kernel<0>, grid, block, 0, s, a);
+    }
     return hipGetLastError();
 }
 
