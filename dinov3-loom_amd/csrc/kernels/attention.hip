@@ -119,8 +119,8 @@ __global__ __launch_bounds__(kThreads, 3) void attention_kernel(AttentionArgs p)
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) qf[kk] = *(const half8_t*)(qg + (size_t)min(qrow, T - 1) * kHeadDim + kk * 16 + hi * 8);
     asm volatile("" ::: "memory");
-    if (nkb > 1) {
-        dma(sK1, sV1, 1);
+    if (NKB == 0 || nkb > 1) {  // with a runtime count, block 1 repeats block 0 when there is one block
+        dma(sK1, sV1, min(1, nkb - 1));
         vm_barrier<kDmaPerBlock>();
     } else {
         vm_barrier<0>();
@@ -222,13 +222,23 @@ __global__ __launch_bounds__(kThreads, 3) void attention_kernel(AttentionArgs p)
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb) step(kbuf[kb % 3], vbuf[kb % 3], kbuf[(kb + 2) % 3], vbuf[(kb + 2) % 3], kb);
     } else {
+        // Runtime block count: every step issues its DMA (past the last block
+        // it repeats the last one into the buffer just released) and waits
+        // the same way, so no branch makes the compiler's counts conservative;
+        // the repeats are drained before the workgroup ends.
+        auto step_rt = [&](const half_t* k_cur, const half_t* v_cur, half_t* k_fill, half_t* v_fill, int kb) {
+            dma(k_fill, v_fill, min(kb + 2, nkb - 1));
+            block(k_cur, v_cur, kb);
+            vm_barrier<kDmaPerBlock>();
+        };
         for (int kb = 0; kb < nkb; kb += 3) {
-            step(sK0, sV0, sK2, sV2, kb);
+            step_rt(sK0, sV0, sK2, sV2, kb);
             if (kb + 1 >= nkb) break;
-            step(sK1, sV1, sK0, sV0, kb + 1);
+            step_rt(sK1, sV1, sK0, sV0, kb + 1);
             if (kb + 2 >= nkb) break;
-            step(sK2, sV2, sK1, sV1, kb + 2);
+            step_rt(sK2, sV2, sK1, sV1, kb + 2);
         }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
 
     if (qrow < T) {
