@@ -2,14 +2,20 @@
 // accumulation, shared by every GEMM variant of the forward pass.
 //
 // A workgroup of WGM x WGN waves owns a BM x BN output tile; the K loop walks
-// BK-wide stages (64 or 32). Stages move HBM/L2 -> registers -> LDS with two
-// register sets and two LDS buffers, so the global loads of stage s+2 are in
-// flight while stage s feeds the MFMAs and stage s+1 is written to LDS. The LDS
-// barrier only waits for LDS traffic (s_waitcnt lgkmcnt(0); s_barrier):
-// __syncthreads() would also drain every outstanding global load (its
-// workgroup release fence waits on vmcnt(0)) and serialise the pipeline.
-// Prefetch loads are unconditional (the stage index is clamped at the end)
-// so the compiler's vmcnt waits count exactly the loads they need.
+// BK-deep stages. Two loops:
+// - gemm_main (the patch embedding): both operands HBM/L2 -> registers ->
+//   LDS (row pitch LDK) with two register sets and two LDS buffers, so the
+//   loads of stage s+2 are in flight while stage s feeds the MFMAs and stage
+//   s+1 is written to LDS.
+// - gemm_main_dma (QKV, residual, SwiGLU, split-K): activations in fragment
+//   order straight into registers (ActFrags), weights in fragment order moved
+//   into three LDS buffers by DMA (WeightDma); its comment has the ordering
+//   rules the waits rely on.
+// The barriers only wait for LDS traffic (and, in the DMA loop, for the DMA
+// loads they must): __syncthreads() would also drain every outstanding
+// global load (its workgroup release fence waits on vmcnt(0)) and serialise
+// the pipeline. Loads are unconditional where possible (indices clamped) so
+// the compiler's vmcnt waits count exactly the loads they need.
 //
 // Each wave owns TM x TN of the tile as 32x32 tiles of
 // v_mfma_f32_32x32x16_f16. The MFMA's first operand is the weight row (n) and
@@ -38,7 +44,6 @@ struct Tile {
     static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile is a multiple of the 32x32 MFMA tile");
     static constexpr int FM = TM / 32, FN = TN / 32;
     static constexpr int STAGE_HALFS = (BM + BN) * LDK;
-    static constexpr int W_HALFS = BN * LDK;  // weight-only stage (activations in registers)
     static constexpr int WF_HALFS = BN * BK;  // weight-only stage in fragment order (WeightDma)
     static constexpr int LDS_HALFS = 2 * STAGE_HALFS;
     static constexpr int LDS_BYTES = LDS_HALFS * 2;
@@ -184,32 +189,10 @@ __device__ __forceinline__ void mma_stage(const half_t* stage, int tid, Acc<T>& 
     }
 }
 
-// mma_stage with the activation fragments already in registers (ActFrags)
-// and only the weight stage in LDS.
-template <class T, class AF>
-__device__ __forceinline__ void mma_stage_areg(const half_t* stage, int tid, const AF& af, Acc<T>& acc) {
-    const int lane = tid & 63, wn = (tid >> 6) / T::WGM;
-    const int l32 = lane & 31, hi = lane >> 5;
-    const half_t* w_s = stage + (wn * T::TN + l32) * T::LDK + hi * 8;
-    half8_t wf[2][T::FN];
-    auto fetch = [&](int kk, int b) {
-#pragma unroll
-        for (int i = 0; i < T::FN; ++i) wf[b][i] = *(const half8_t*)(w_s + i * 32 * T::LDK + kk * 16);
-    };
-    fetch(0, 0);
-#pragma unroll
-    for (int kk = 0; kk < T::BK / 16; ++kk) {
-        if (kk + 1 < T::BK / 16) fetch(kk + 1, (kk + 1) & 1);
-#pragma unroll
-        for (int i = 0; i < T::FN; ++i)
-#pragma unroll
-            for (int j = 0; j < T::FM; ++j) acc.v[i][j] = mfma32x32x16(wf[kk & 1][i], af.f[j][kk], acc.v[i][j]);
-    }
-}
-
-// mma_stage_areg with the weight stage in fragment order (WeightDma): the
+// One stage of MFMAs with the activation fragments already in registers
+// (ActFrags) and the weight stage in LDS in fragment order (WeightDma): the
 // wave reads every column of the stage (WGN == 1), one contiguous 1 KB block
-// per fragment.
+// per fragment, for k-slice kk+1 while kk computes.
 template <class T, class AF>
 __device__ __forceinline__ void mma_stage_frag(const half_t* stage, int tid, const AF& af, Acc<T>& acc) {
     constexpr int KS = T::BK / 16;
@@ -286,57 +269,30 @@ __device__ __forceinline__ void gemm_main(AL (&al)[P], WL (&wl)[P], int m0, int 
 #pragma unroll
         for (int j = 0; j < T::FM; ++j) acc.v[i][j] = float16_t{};
     const int last = k_tiles - 1;
-    if constexpr (AL::kInRegs) {
-        // Activations in registers, only W through LDS: register set b of
-        // both operands holds the stage computed from LDS buffer b; a set is
-        // refilled (two stages ahead) once that stage's MFMAs have read it.
-        half_t* const s0 = lds;
-        half_t* const s1 = lds + T::W_HALFS;
-        al[0].load(m0, n0, 0, tid);
-        wl[0].load(m0, n0, 0, tid);
-        al[1].load(m0, n0, min(1, last), tid);
-        wl[1].load(m0, n0, min(1, last), tid);
-        settle();
-        wl[0].store(s0, tid);
-        lds_barrier();
-        for (int kt = 0; kt < k_tiles; kt += 2) {
-            wl[0].load(m0, n0, min(kt + 2, last), tid);
-            mma_stage_areg<T>(s0, tid, al[0], acc);
-            al[0].load(m0, n0, min(kt + 2, last), tid);
-            wl[1].store(s1, tid);
-            lds_barrier();
-            wl[1].load(m0, n0, min(kt + 3, last), tid);
-            mma_stage_areg<T>(s1, tid, al[1], acc);
-            al[1].load(m0, n0, min(kt + 3, last), tid);
-            if (kt + 2 < k_tiles) wl[0].store(s0, tid);
-            lds_barrier();
-        }
-    } else {
 #pragma unroll
-        for (int i = 0; i < P; ++i) {
-            al[i].load(m0, n0, min(i, last), tid);
-            wl[i].load(m0, n0, min(i, last), tid);
-        }
-        settle();
-        al[0].store(lds, tid);
-        wl[0].store(lds + T::BM * T::LDK, tid);
-        lds_barrier();
-        for (int base = 0; base < k_tiles; base += 2) {
+    for (int i = 0; i < P; ++i) {
+        al[i].load(m0, n0, min(i, last), tid);
+        wl[i].load(m0, n0, min(i, last), tid);
+    }
+    settle();
+    al[0].store(lds, tid);
+    wl[0].store(lds + T::BM * T::LDK, tid);
+    lds_barrier();
+    for (int base = 0; base < k_tiles; base += 2) {
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int s = base + i;
-                if (s >= k_tiles) break;  // uniform
-                half_t* const cur = lds + i * T::STAGE_HALFS;
-                half_t* const nxt = lds + (1 - i) * T::STAGE_HALFS;
-                al[i].load(m0, n0, min(s + 2, last), tid);
-                wl[i].load(m0, n0, min(s + 2, last), tid);
-                mma_stage<T>(cur, tid, acc);
-                if (s + 1 < k_tiles) {
-                    al[1 - i].store(nxt, tid);
-                    wl[1 - i].store(nxt + T::BM * T::LDK, tid);
-                }
-                lds_barrier();
+        for (int i = 0; i < 2; ++i) {
+            const int s = base + i;
+            if (s >= k_tiles) break;  // uniform
+            half_t* const cur = lds + i * T::STAGE_HALFS;
+            half_t* const nxt = lds + (1 - i) * T::STAGE_HALFS;
+            al[i].load(m0, n0, min(s + 2, last), tid);
+            wl[i].load(m0, n0, min(s + 2, last), tid);
+            mma_stage<T>(cur, tid, acc);
+            if (s + 1 < k_tiles) {
+                al[1 - i].store(nxt, tid);
+                wl[1 - i].store(nxt + T::BM * T::LDK, tid);
             }
+            lds_barrier();
         }
     }
 }
