@@ -2,7 +2,7 @@
 // kernels/attention_online_f16_wmma_cf16.loom).
 //
 // One workgroup = 4 waves = 128 queries of one (image, head); each wave owns
-// 32 queries. Keys stream through LDS in blocks of 64 (K and V both as
+// 32 queries. Keys stream through LDS in blocks of 32 or 64 (K and V both as
 // [key][ch]), so the same kernel serves 201 tokens (224x224) and 1029
 // tokens (512x512). The blocks move from global memory straight into three
 // LDS buffers with DMA loads (buffer_load ... lds), two blocks ahead; each
@@ -29,8 +29,6 @@ namespace dhx {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int KB = 64;                   // keys per LDS block
-constexpr int BLK = KB * kHeadDim;       // halfs per K (or V) block
 constexpr int QB = 128;                  // queries per workgroup
 constexpr float kLazy = 8.0f;            // running-max slack of the lazy rescaling (score units)
 
@@ -63,13 +61,22 @@ __device__ __forceinline__ void vm_barrier() {
     asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
-// NKB > 0: the number of key blocks, known at compile time (the block loop is
-// then unrolled, which keeps the compiler's wait counts exact; used for the
-// four blocks of 201 tokens); 0: any.
+// NKB > 0: the number of key blocks of KB = 32 keys, known at compile time
+// (the block loop is then unrolled, which keeps the compiler's wait counts
+// exact; used for 201 tokens, whose 24 KB of LDS also leave room for other
+// image groups' kernels). NKB = 0: any count of KB = 64-key blocks.
+template <int NKB>
+struct KeyBlock {
+    static constexpr int KB = NKB > 0 ? 32 : 64;   // keys per LDS block
+    static constexpr int BLK = KB * kHeadDim;      // halfs per K (or V) block
+    static constexpr int LOADS = KB / 32;          // DMA loads of 8 rows per matrix and wave
+};
+
 template <int NKB>
 __global__ __launch_bounds__(kThreads, 3) void attention_kernel(AttentionArgs p) {
-    __shared__ __attribute__((aligned(16))) half_t sK0[BLK], sK1[BLK], sK2[BLK];
-    __shared__ __attribute__((aligned(16))) half_t sV0[BLK], sV1[BLK], sV2[BLK];
+    using KBT = KeyBlock<NKB>;
+    __shared__ __attribute__((aligned(16))) half_t sK0[KBT::BLK], sK1[KBT::BLK], sK2[KBT::BLK];
+    __shared__ __attribute__((aligned(16))) half_t sV0[KBT::BLK], sV1[KBT::BLK], sV2[KBT::BLK];
     // 1-D grid, XCD-aware: the tile space (query block fastest, then head,
     // then image) is cut into 8 contiguous chunks, one per XCD, so the query
     // blocks of one (image, head) share K and V in that XCD's L2.
@@ -82,7 +89,7 @@ __global__ __launch_bounds__(kThreads, 3) void attention_kernel(AttentionArgs p)
     const int T = p.tokens;
     const size_t bh = (size_t)img * kHeads + head;
     const half_t* qg = p.q + bh * p.tpad * kHeadDim;
-    const int nkb = NKB > 0 ? NKB : (T + KB - 1) / KB;  // nkb * KB <= tpad, so every block row exists
+    const int nkb = NKB > 0 ? NKB : (T + KBT::KB - 1) / KBT::KB;  // nkb * KB <= tpad, so every block row exists
 
     // Block kb of K and V: wave w moves key rows 16w .. 16w+15 of each, as
     // two 1 KB DMA loads per matrix (8 rows each). Lane i lands at LDS slot
@@ -93,20 +100,26 @@ __global__ __launch_bounds__(kThreads, 3) void attention_kernel(AttentionArgs p)
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<half_t*>(p.v + bh * p.tpad * kHeadDim), 0, bytes, kBufferRsrcWord3);
     // Load j covers rows 16w + 8j .. +7 (row % 16 = 8j + lane / 8).
+    // Wave w moves key rows (KB/4) w .. +KB/4-1 as KB/32 loads of 8 rows
+    // per matrix; load j covers rows r0 = (KB/4) w + 8j, so row % 16 =
+    // r0 % 16 + lane / 8.
+    // Sized 2, not KBT::LOADS: with a local array whose size depends on the
+    // template parameter this compiler silently drops the host launch stub.
     int voff[2];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) voff[j] = (lane >> 3) * 128 + (((lane & 7) ^ swz_slot(j * 8 + (lane >> 3))) << 4);
+    for (int j = 0; j < KBT::LOADS; ++j)
+        voff[j] = (lane >> 3) * 128 + (((lane & 7) ^ swz_slot(((tid >> 6) * (KBT::KB / 4) + 8 * j) % 16 + (lane >> 3))) << 4);
     auto dma = [&](half_t* k_buf, half_t* v_buf, int kb) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int row = wave * 16 + j * 8, soff = (kb * KB + row) * 128;
+        for (int j = 0; j < KBT::LOADS; ++j) {
+            const int row = wave * (KBT::KB / 4) + j * 8, soff = (kb * KBT::KB + row) * 128;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(k_buf + row * kHeadDim),
                                                      16, voff[j], soff, 0, 0);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)(v_buf + row * kHeadDim),
                                                      16, voff[j], soff, 0, 0);
         }
     };
-    constexpr int kDmaPerBlock = 4;  // per wave
+    constexpr int kDmaPerBlock = 2 * KBT::LOADS;  // per wave
 
     // Block 0 first, then the Q fragments (registers), then block 1: the
     // wait for block 0 counts only the DMA loads of block 1 (DMA loads land
@@ -144,8 +157,8 @@ __global__ __launch_bounds__(kThreads, 3) void attention_kernel(AttentionArgs p)
 
     auto block = [&](const half_t* sK, const half_t* sV, int kb) {
 #pragma unroll
-        for (int sub = 0; sub < 2 && active; ++sub) {
-            const int key0 = kb * KB + sub * 32;
+        for (int sub = 0; sub < KBT::KB / 32 && active; ++sub) {
+            const int key0 = kb * KBT::KB + sub * 32;
             if (key0 >= T) break;  // uniform across the workgroup
             float16_t s = {};
             const int kr = sub * 32 + l32;
@@ -267,9 +280,11 @@ __global__ __launch_bounds__(kThreads, 3) void attention_kernel(AttentionArgs p)
 hipError_t launch_attention(const AttentionArgs& a, hipStream_t s) {
     const int total = (a.tokens + QB - 1) / QB * kHeads * a.images;
     const dim3 grid((total + 7) & ~7), block(kThreads);
-    switch ((a.tokens + KB - 1) / KB) {
-        case 4:  // 224x224: 201 tokens
-            hipLaunchKernelGGL(attention_kernel<4>, grid, block, 0, s, a);
+    // 224x224 (201 tokens): seven blocks of 32 keys, unrolled; otherwise blocks
+    // of 64 with a run-time count.
+    switch ((a.tokens + 31) / 32) {
+        case 7:
+            hipLaunchKernelGGL(attention_kernel<7>, grid, block, 0, s, a);
             break;
         default:
             hipLaunchKernelGGL(attention_kernel<0>, grid, block, 0, s, a);
