@@ -81,6 +81,19 @@ def timed_replays(model, b, steps):
     return (time.perf_counter() - t0) / steps
 
 
+def replay_latency(model, b, samples):
+    """Median host-clock time of one synchronised replay (the reference's
+    ForwardTimings scope, engine.rs:130-190)."""
+    t = []
+    for _ in range(samples):
+        model.synchronize()
+        t0 = time.perf_counter()
+        model.replay(b)
+        model.synchronize()
+        t.append(time.perf_counter() - t0)
+    return sorted(t)[len(t) // 2]
+
+
 def cpu_baseline(path, seconds):
     """The float64 C oracle on this host: one thread (the `cpu_baseline`
     object, like the reference's single-threaded oracle) and, beside it, all
@@ -204,6 +217,13 @@ def main():
         sec32 = timed_replays(model, 32, args.steps)
         model.set_branches(branches)
 
+        # Batch 1 (the reference's own benchmark case: graph-replay latency of
+        # one image, split-K down projection as in lib.rs:218-225).
+        model.stage(px[:1])
+        for _ in range(args.warmup):
+            model.replay(1)
+        sec1 = replay_latency(model, 1, args.steps)
+
         # End to end through the host API (PCIe-inclusive; never `value`):
         # forward() of 4 chunks of b images from host memory to host memory,
         # with the pipelined uploads and readbacks.
@@ -286,6 +306,8 @@ def main():
                    "weights": "seeded random init (BASELINE)"},
         "mfma_frac_forward": round(value * GFLOP_PER_IMAGE / 1e3 / PEAK_TFLOPS, 4),
         "batch32": {"value": round(32 / sec32, 1), "ms_per_step": round(sec32 * 1e3, 4), "branches": branches32},
+        "batch1": {"value": round(1 / sec1, 1), "ms_per_step": round(sec1 * 1e3, 4),
+                   "what": "median synchronised graph-replay latency of one image (the reference's b = 1 case)"},
         "highres_512_b8": {"value": round(8 / sec_hr, 1), "unit": "images/s", "ms_per_step": round(sec_hr * 1e3, 4),
                            "branches": branches_hr, "what": "BASELINE.json config 4: 512x512, 1029 tokens, batch 8"},
         "end_to_end": {"value": round(e2e_rate, 1), "unit": "images/s",
