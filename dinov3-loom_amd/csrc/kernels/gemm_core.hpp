@@ -349,7 +349,9 @@ __device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory")
 // (both released by the previous barrier), computes stage s, and ends with a
 // barrier that waits until only the DMA of stage s+2 may be outstanding:
 // by DMA order stage s+1 has then landed for every wave. Activations get
-// one step to arrive, weights two. The three buffers are separate LDS
+// one step to arrive, weights up to two (the compiler places the DMA
+// instructions among the step's last MFMAs; holding them at the top of the
+// step with a scheduling barrier measured no faster). The three buffers are separate LDS
 // variables and the loop is unrolled over them, so the compiler can tell a
 // buffer being read from the ones being filled and does not wait for the
 // DMA in flight. Nothing is loaded past the last stage. With KT > 0 the
