@@ -91,15 +91,14 @@ __global__ __launch_bounds__(kThreads, 3) void attention_kernel(AttentionArgs p)
     const half_t* qg = p.q + bh * p.tpad * kHeadDim;
     const int nkb = NKB > 0 ? NKB : (T + KBT::KB - 1) / KBT::KB;  // nkb * KB <= tpad, so every block row exists
 
-    // Block kb of K and V: wave w moves key rows 16w .. 16w+15 of each, as
-    // two 1 KB DMA loads per matrix (8 rows each). Lane i lands at LDS slot
-    // (row i/8, chunk slot i%8) and fetches the chunk the swizzle puts there.
+    // Block kb of K and V: each wave moves KB/4 key rows of each, as 1 KB
+    // DMA loads of 8 rows. Lane i lands at LDS slot (row i/8, chunk slot
+    // i%8) and fetches the chunk the swizzle puts there.
     const uint32_t bytes = (uint32_t)p.tpad * kHeadDim * 2;
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<half_t*>(p.k + bh * p.tpad * kHeadDim), 0, bytes, kBufferRsrcWord3);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<half_t*>(p.v + bh * p.tpad * kHeadDim), 0, bytes, kBufferRsrcWord3);
-    // Load j covers rows 16w + 8j .. +7 (row % 16 = 8j + lane / 8).
     // Wave w moves key rows (KB/4) w .. +KB/4-1 as KB/32 loads of 8 rows
     // per matrix; load j covers rows r0 = (KB/4) w + 8j, so row % 16 =
     // r0 % 16 + lane / 8.
