@@ -32,11 +32,6 @@ constexpr int kThreads = 256;
 constexpr int QB = 128;                  // queries per workgroup
 constexpr float kLazy = 8.0f;            // running-max slack of the lazy rescaling (score units)
 
-__device__ __forceinline__ half8_t zero8() {
-    half8_t z = {};
-    return z;
-}
-
 // LDS on gfx950 has 64 banks of 4 bytes: two 128-byte key rows per bank
 // cycle. Chunk c of key row r sits at slot c ^ swz_slot(r), with
 // swz_slot(r) = f((r / 2) % 8), f(t) = 4 (t % 2) + t / 2 (a bijection). The
