@@ -211,14 +211,15 @@ def main():
 
         # Batch 32 (config 2) on the same resident model, with its own short
         # trial of the image grouping.
+        px32 = px[:32] if b >= 32 else d.random_pixels(1, 32)
         trial32 = {}
         for nb in ([args.branches] if args.branches else [1, 2, 3, 4]):
             model.set_branches(nb)
-            model.stage(px[:32])
+            model.stage(px32)
             trial32[nb] = timed_replays(model, 32, 10)
         branches32 = min(trial32, key=trial32.get)
         model.set_branches(branches32)
-        model.stage(px[:32])
+        model.stage(px32)
         for _ in range(args.warmup):
             model.replay(32)
         sec32 = timed_replays(model, 32, args.steps)
