@@ -22,6 +22,7 @@ constexpr int kPrefix = 5;
 constexpr int kFF = 1536;
 constexpr int kWave = 64;
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
 // Word 3 of a raw buffer descriptor on CDNA (gfx9 family): 32-bit data
 // format (untyped buffer instructions need a nonzero one), no swizzle, no
 // index stride.
@@ -120,9 +121,6 @@ __device__ __forceinline__ half8_t frag_swap(half4_t g0, half4_t g1) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
-
-// silu(g) = g / (1 + e^-g), with e^-g evaluated as 2^(-g * log2 e) on v_exp_f32.
-__device__ __forceinline__ float silu(float g) { return g * fast_rcp(1.0f + fast_exp2(-g * kLog2e)); }
 
 // Fragment order of an f16 activation matrix A[rows][K] (K a multiple of 16;
 // rows padded to a multiple of 32): fragment (mb, ks) holds rows 32mb ..

@@ -388,7 +388,9 @@ __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void swiglu_kernel(
         },
         [&] {
             if (tid < T::BN) {
-                cst[0][tid] = cb;
+                // Gate columns (the first 32 of each 64) are kept scaled by
+                // -log2(e), up columns by -ln(2); see the epilogue.
+                cst[0][tid] = cb * (tid % 64 < 32 ? -kLog2e : -kLn2);
                 cst[1][tid] = cw;
             }
 #pragma unroll
@@ -399,10 +401,16 @@ __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void swiglu_kernel(
         const int lane = threadIdx.x & 63, mblocks = (p.rows + 31) / 32;
         // Pair q of the wave: gate = acc.v[2q], up = acc.v[2q + 1], outputs
         // 32q .. 32q+31 of the wave's OW, i.e. act fragments 2q and 2q + 1.
+        // With gate g and up u (after LayerNorm folding and bias), the output
+        // silu(g) u = g u / (1 + e^-g) is computed from gs = -g log2(e) and
+        // us = -u ln(2) as gs us / (1 + 2^gs) (gs us = g u): the scales ride
+        // on the FMAs that apply rstd and the bias, which saves the multiply
+        // that would otherwise form the exponent.
 #pragma unroll
         for (int j = 0; j < T::FM; ++j) {
             const int mb = f.m_base / 32 + j;
             if (mb >= mblocks) break;  // uniform per wave
+            const float sg = rn[j].rstd * -kLog2e, su = rn[j].rstd * -kLn2;
 #pragma unroll
             for (int q = 0; q < T::FN / 2; ++q) {
                 half4_t y[4];
@@ -411,12 +419,15 @@ __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void swiglu_kernel(
                     const int c = g * 8 + f.hi * 4, nl = f.n_base - n0 + 64 * q + c;
                     float4_t gate = group4(acc.v[2 * q][j], g), up = group4(acc.v[2 * q + 1][j], g);
                     if constexpr (LN) {
-                        gate = (gate - rn[j].mean * *(const float4_t*)&cst[1][nl]) * rn[j].rstd;
-                        up = (up - rn[j].mean * *(const float4_t*)&cst[1][nl + 32]) * rn[j].rstd;
+                        gate -= rn[j].mean * *(const float4_t*)&cst[1][nl];
+                        up -= rn[j].mean * *(const float4_t*)&cst[1][nl + 32];
                     }
-                    gate += *(const float4_t*)&cst[0][nl];
-                    up += *(const float4_t*)&cst[0][nl + 32];
-                    y[g] = to_half4(float4_t{silu(gate[0]), silu(gate[1]), silu(gate[2]), silu(gate[3])} * up);
+                    const float4_t gs = gate * sg + *(const float4_t*)&cst[0][nl];
+                    const float4_t us = up * su + *(const float4_t*)&cst[0][nl + 32];
+                    float4_t r;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) r[e] = gs[e] * us[e] * fast_rcp(1.0f + fast_exp2(gs[e]));
+                    y[g] = to_half4(r);
                 }
 #pragma unroll
                 for (int kk = 0; kk < 2; ++kk)
