@@ -273,7 +273,7 @@ __global__ __launch_bounds__(T::THREADS, T::BK == 128 ? 3 : 4) void resid_kernel
     static_assert(T::BN <= T::THREADS, "one thread per column constant");
     constexpr int XF = T::TN / 16;  // x fragments per wave
     __shared__ __attribute__((aligned(16))) half_t wb0[T::WF_HALFS], wb1[T::WF_HALFS], wb2[T::WF_HALFS];
-    __shared__ __attribute__((aligned(16))) float cst[2][T::BN];  // bias, ls of the tile's columns
+    __shared__ __attribute__((aligned(16))) float cst[2][T::BN];  // bias * ls, ls of the tile's columns
     constexpr int NT = kHidden / T::BN;
     const int tid = threadIdx.x, lane = tid & 63, mblocks = (p.rows + 31) / 32;
     ActFrags<T> al[2];
@@ -302,7 +302,7 @@ __global__ __launch_bounds__(T::THREADS, T::BK == 128 ? 3 : 4) void resid_kernel
         },
         [&] {
             if (tid < T::BN) {
-                cst[0][tid] = cb;
+                cst[0][tid] = cb * cl;  // ls * (acc + b) = acc * ls + b * ls: one FMA per output
                 cst[1][tid] = cl;
             }
         },
@@ -321,8 +321,8 @@ __global__ __launch_bounds__(T::THREADS, T::BK == 128 ? 3 : 4) void resid_kernel
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const int nt = f.col(i, g) - n0;  // column in the tile
-                    const float4_t b = *(const float4_t*)&cst[0][nt], l = *(const float4_t*)&cst[1][nt];
-                    u[g] = (group4(acc.v[i][0], g) + b) * l;
+                    const float4_t bl = *(const float4_t*)&cst[0][nt], l = *(const float4_t*)&cst[1][nt];
+                    u[g] = group4(acc.v[i][0], g) * l + bl;
                 }
                 frag_swap(u[0], u[1]);
                 frag_swap(u[2], u[3]);
