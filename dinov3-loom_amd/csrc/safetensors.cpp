@@ -1,5 +1,6 @@
 #include "safetensors.hpp"
 
+#include <algorithm>
 #include <cerrno>
 #include <cstdio>
 #include <cstring>
@@ -100,25 +101,40 @@ private:
             }
             fail("bad literal");
         } else if (c == '-' || (c >= '0' && c <= '9')) {
+            // JSON number grammar: -?(0|[1-9][0-9]*)(.[0-9]+)?([eE][+-]?[0-9]+)?
+            // Only a plain non-negative integer that fits 64 bits is an
+            // integer (shapes and offsets must be).
             v.kind = Json::Number;
-            const char* start = p_;
             bool integer = true;
             if (*p_ == '-') {
                 integer = false;
                 ++p_;
             }
+            auto digit = [&] { return p_ < end_ && *p_ >= '0' && *p_ <= '9'; };
+            if (!digit()) fail("bad number");
             uint64_t acc = 0;
-            while (p_ < end_ && ((*p_ >= '0' && *p_ <= '9') || *p_ == '.' || *p_ == 'e' || *p_ == 'E' ||
-                                 *p_ == '+' || *p_ == '-')) {
-                if (*p_ >= '0' && *p_ <= '9') {
-                    if (acc > (UINT64_MAX - 9) / 10) fail("number too large");
-                    acc = acc * 10 + (uint64_t)(*p_ - '0');
-                } else {
-                    integer = false;
-                }
+            if (*p_ == '0') {
                 ++p_;
+            } else {
+                while (digit()) {
+                    const uint64_t dgt = (uint64_t)(*p_++ - '0');
+                    if (acc > (UINT64_MAX - dgt) / 10) integer = false;  // does not fit u64
+                    else acc = acc * 10 + dgt;
+                }
             }
-            if (p_ == start) fail("bad number");
+            if (p_ < end_ && *p_ == '.') {
+                integer = false;
+                ++p_;
+                if (!digit()) fail("bad number");
+                while (digit()) ++p_;
+            }
+            if (p_ < end_ && (*p_ == 'e' || *p_ == 'E')) {
+                integer = false;
+                ++p_;
+                if (p_ < end_ && (*p_ == '+' || *p_ == '-')) ++p_;
+                if (!digit()) fail("bad number");
+                while (digit()) ++p_;
+            }
             v.integer = acc;
             v.is_integer = integer;
         } else {
@@ -126,6 +142,19 @@ private:
         }
         --depth_;
         return v;
+    }
+    uint32_t hex4() {
+        if (end_ - p_ < 4) fail("bad unicode escape");
+        uint32_t cp = 0;
+        for (int i = 0; i < 4; ++i) {
+            const char h = *p_++;
+            cp <<= 4;
+            if (h >= '0' && h <= '9') cp |= h - '0';
+            else if (h >= 'a' && h <= 'f') cp |= h - 'a' + 10;
+            else if (h >= 'A' && h <= 'F') cp |= h - 'A' + 10;
+            else fail("bad unicode escape");
+        }
+        return cp;
     }
     std::string string() {
         expect('"');
@@ -145,23 +174,27 @@ private:
                     case 'r': out += '\r'; break;
                     case 't': out += '\t'; break;
                     case 'u': {
-                        if (end_ - p_ < 4) fail("bad unicode escape");
-                        unsigned cp = 0;
-                        for (int i = 0; i < 4; ++i) {
-                            const char h = *p_++;
-                            cp <<= 4;
-                            if (h >= '0' && h <= '9') cp |= h - '0';
-                            else if (h >= 'a' && h <= 'f') cp |= h - 'a' + 10;
-                            else if (h >= 'A' && h <= 'F') cp |= h - 'A' + 10;
-                            else fail("bad unicode escape");
+                        uint32_t cp = hex4();
+                        if (cp >= 0xdc00 && cp <= 0xdfff) fail("lone surrogate");
+                        if (cp >= 0xd800 && cp <= 0xdbff) {  // a pair: \uD8xx\uDCxx
+                            if (end_ - p_ < 2 || p_[0] != '\\' || p_[1] != 'u') fail("lone surrogate");
+                            p_ += 2;
+                            const uint32_t lo = hex4();
+                            if (lo < 0xdc00 || lo > 0xdfff) fail("lone surrogate");
+                            cp = 0x10000 + ((cp - 0xd800) << 10) + (lo - 0xdc00);
                         }
                         if (cp < 0x80) {
                             out += (char)cp;
                         } else if (cp < 0x800) {
                             out += (char)(0xc0 | (cp >> 6));
                             out += (char)(0x80 | (cp & 0x3f));
-                        } else {
+                        } else if (cp < 0x10000) {
                             out += (char)(0xe0 | (cp >> 12));
+                            out += (char)(0x80 | ((cp >> 6) & 0x3f));
+                            out += (char)(0x80 | (cp & 0x3f));
+                        } else {
+                            out += (char)(0xf0 | (cp >> 18));
+                            out += (char)(0x80 | ((cp >> 12) & 0x3f));
                             out += (char)(0x80 | ((cp >> 6) & 0x3f));
                             out += (char)(0x80 | (cp & 0x3f));
                         }
@@ -170,6 +203,7 @@ private:
                     default: fail("bad escape");
                 }
             } else {
+                if ((unsigned char)*p_ < 0x20) fail("control character in string");
                 out += *p_++;
             }
         }
@@ -179,12 +213,43 @@ private:
     }
 };
 
-uint64_t dtype_size(const std::string& d) {
-    if (d == "F64" || d == "I64" || d == "U64") return 8;
-    if (d == "F32" || d == "I32" || d == "U32") return 4;
-    if (d == "F16" || d == "BF16" || d == "I16" || d == "U16") return 2;
-    if (d == "I8" || d == "U8" || d == "BOOL" || d == "F8_E4M3" || d == "F8_E5M2") return 1;
+// Bits per element of the dtypes the format defines (safetensors 0.6
+// `Dtype::bitsize`); the loader itself only widens F32, F16 and BF16.
+uint64_t dtype_bits(const std::string& d) {
+    if (d == "F64" || d == "I64" || d == "U64" || d == "C64") return 64;
+    if (d == "F32" || d == "I32" || d == "U32") return 32;
+    if (d == "F16" || d == "BF16" || d == "I16" || d == "U16") return 16;
+    if (d == "I8" || d == "U8" || d == "BOOL" || d == "F8_E4M3" || d == "F8_E5M2" || d == "F8_E8M0") return 8;
+    if (d == "F6_E2M3" || d == "F6_E3M2") return 6;
+    if (d == "F4") return 4;
     throw Error("invalid safetensors header: unknown dtype " + d);
+}
+
+// RFC 3629 UTF-8 (no overlongs, no surrogates, at most U+10FFFF): the crate
+// reads the header as a Rust str.
+bool valid_utf8(const uint8_t* s, uint64_t n) {
+    uint64_t i = 0;
+    while (i < n) {
+        const uint8_t c = s[i];
+        if (c < 0x80) {
+            ++i;
+            continue;
+        }
+        int len;
+        uint32_t cp, min;
+        if ((c & 0xe0) == 0xc0) len = 2, cp = c & 0x1f, min = 0x80;
+        else if ((c & 0xf0) == 0xe0) len = 3, cp = c & 0x0f, min = 0x800;
+        else if ((c & 0xf8) == 0xf0) len = 4, cp = c & 0x07, min = 0x10000;
+        else return false;
+        if (n - i < (uint64_t)len) return false;
+        for (int k = 1; k < len; ++k) {
+            if ((s[i + k] & 0xc0) != 0x80) return false;
+            cp = (cp << 6) | (s[i + k] & 0x3f);
+        }
+        if (cp < min || cp > 0x10ffff || (cp >= 0xd800 && cp <= 0xdfff)) return false;
+        i += len;
+    }
+    return true;
 }
 
 }  // namespace
@@ -201,18 +266,39 @@ std::vector<uint8_t> read_file(const std::string& path) {
     return data;
 }
 
+// The checks of the safetensors crate (0.6, `SafeTensors::read_metadata` and
+// `Metadata::validate`): header length at most 100,000,000 bytes and within
+// the file, a UTF-8 JSON object starting with '{', string-valued
+// __metadata__, unique tensor names, and data ranges that, sorted by offset,
+// tile the data section exactly from 0 to its end (no gaps, overlaps or
+// trailing bytes), each range holding exactly shape x dtype bytes.
 SafeTensors::SafeTensors(std::vector<uint8_t> file) : file_(std::move(file)) {
+    constexpr uint64_t kMaxHeader = 100000000;
     if (file_.size() < 8) throw Error("invalid safetensors header: file too small");
     uint64_t n = 0;
     for (int i = 7; i >= 0; --i) n = (n << 8) | file_[i];
-    if (n > 100u * 1024 * 1024 || n > file_.size() - 8) throw Error("invalid safetensors header: bad header length");
+    if (n > kMaxHeader) throw Error("invalid safetensors header: header too large");
+    if (n > file_.size() - 8) throw Error("invalid safetensors header: bad header length");
+    if (n == 0 || file_[8] != '{') throw Error("invalid safetensors header: does not start with {");
+    if (!valid_utf8(file_.data() + 8, n)) throw Error("invalid safetensors header: not UTF-8");
     const char* h = reinterpret_cast<const char*>(file_.data() + 8);
     Json doc = Parser(h, h + n).parse_document();
     if (doc.kind != Json::Object) throw Error("invalid safetensors header: not an object");
     const uint8_t* base = file_.data() + 8 + n;
     const uint64_t data_bytes = file_.size() - 8 - n;
+    struct Range {
+        uint64_t begin, end;
+        const std::string* name;
+    };
+    std::vector<Range> ranges;
     for (auto& kv : doc.members) {
-        if (kv.first == "__metadata__") continue;
+        if (kv.first == "__metadata__") {
+            if (kv.second.kind != Json::Object) throw Error("invalid safetensors header: __metadata__");
+            for (auto& m : kv.second.members)
+                if (m.second.kind != Json::String) throw Error("invalid safetensors header: __metadata__ value " + m.first);
+            continue;
+        }
+        if (tensors_.count(kv.first)) throw Error("invalid safetensors header: duplicate tensor " + kv.first);
         const Json& t = kv.second;
         if (t.kind != Json::Object) throw Error("invalid safetensors header: tensor " + kv.first);
         TensorView view;
@@ -241,13 +327,23 @@ SafeTensors::SafeTensors(std::vector<uint8_t> file) : file_(std::move(file)) {
             if (d != 0 && numel > UINT64_MAX / d) throw Error("invalid safetensors header: shape of " + kv.first);
             numel *= d;
         }
-        const uint64_t esize = dtype_size(view.dtype);
-        if (numel > UINT64_MAX / esize || numel * esize != e.integer - b.integer)
-            throw Error("invalid safetensors header: size of " + kv.first);
+        const uint64_t bits = dtype_bits(view.dtype);
+        if (numel > UINT64_MAX / bits) throw Error("invalid safetensors header: shape of " + kv.first);
+        if (numel * bits % 8 != 0) throw Error("invalid safetensors header: misaligned size of " + kv.first);
+        if (numel * bits / 8 != e.integer - b.integer) throw Error("invalid safetensors header: size of " + kv.first);
         view.data = base + b.integer;
         view.bytes = e.integer - b.integer;
-        tensors_[kv.first] = std::move(view);
+        auto it = tensors_.emplace(kv.first, std::move(view)).first;
+        ranges.push_back({b.integer, e.integer, &it->first});
     }
+    std::sort(ranges.begin(), ranges.end(),
+              [](const Range& x, const Range& y) { return x.begin != y.begin ? x.begin < y.begin : x.end < y.end; });
+    uint64_t at = 0;
+    for (const Range& r : ranges) {
+        if (r.begin != at) throw Error("invalid safetensors header: offsets of " + *r.name);
+        at = r.end;
+    }
+    if (at != data_bytes) throw Error("invalid safetensors header: data section is not exactly covered by tensors");
 }
 
 const TensorView* SafeTensors::find(const std::string& name) const {

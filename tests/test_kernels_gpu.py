@@ -480,17 +480,142 @@ def test_swiglu_layernorm_fused(eng, rows, offset):
     check(y, ref, atol=3e-3, what=f"fused-LN swiglu rows={rows}")
 
 
-# ---------------------------------------------------------------------------
-# Bitwise repeatability of the GEMM kernels at the batch-64 shapes. The GEMMs
-# move their weight stages into LDS with DMA loads; waiting for one correctly
-# depends on the order in which those loads and the register loads complete,
-# and a wrong wait shows up as results that change from launch to launch
-# (stale weights in LDS), not as a fault.
+def adversarial_rows(rng, rows, case):
+    """Residual-stream rows that stress LayerNorm folded into a GEMM
+    (out = rstd * (x.W'^T - mean * wsum) + t cancels when |mean| >> std):
+    'offset' rows have |mean| / std of 50-200 (std 0.5-2, mean +-25..+-400);
+    'outlier' rows are N(0, 1) with 2-4 channels at +-200 (the high-norm
+    channels of real checkpoints); 'both' mixes the two with ordinary rows."""
+    x = rng.normal(size=(rows, 384))
+    kind = np.arange(rows) % 3 if case == "both" else np.full(rows, {"offset": 1, "outlier": 2}[case])
+    for r in range(rows):
+        if kind[r] == 1:
+            std = rng.uniform(0.5, 2.0)
+            x[r] = x[r] * std + rng.choice([-1, 1]) * std * rng.uniform(50, 200)
+        elif kind[r] == 2:
+            ch = rng.choice(384, size=rng.integers(2, 5), replace=False)
+            x[r, ch] = rng.choice([-200.0, 200.0], size=ch.size)
+    return f16(x)
 
+
+@pytest.mark.parametrize("case", ["offset", "outlier", "both"])
+def test_qkv_rope_layernorm_fused_adversarial(eng, case):
+    # The folded plan against the oracle (LN of the same f16 x in float64,
+    # then the f32 weights) and against the unfused plan's kernels (LayerNorm
+    # to f16 h, then QKV on h) on the same rows: the folded result must be at
+    # least as close to the oracle as the unfused one, within the per-kernel
+    # bar. Reference rounding point: layernorm_rowwave_f16.loom:86-93.
+    rng = np.random.default_rng({"offset": 1, "outlier": 2, "both": 3}[case])
+    images, grid = 3, 14
+    T = grid * grid + 5
+    tpad = (T + 127) // 128 * 128
+    x = adversarial_rows(rng, images * T, case)
+    gamma = (1 + rng.normal(size=384) * 0.2).astype(np.float32)
+    beta = (rng.normal(size=384) * 0.2).astype(np.float32)
+    w = (rng.normal(size=(1152, 384)) * 0.05).astype(np.float32)
+    b = (rng.normal(size=1152) * 0.1).astype(np.float32)
+    wl, wsum, t = fold(w, b, gamma, beta)
+    cos, sin = oracle.rope_tables(grid)
+    nb = images * 6 * tpad * 64 * 2
+    qkv_f = [eng.allocate(nb) for _ in range(3)]
+    qkv_u = [eng.allocate(nb) for _ in range(3)]
+    X, C, S = upf(eng, x), up(eng, cos), up(eng, sin)
+    run(eng, K_QKV_LN, [images, grid, tpad],
+        [X, up(eng, slot_stats(x)), upf(eng, wl), up(eng, wsum), up(eng, t), C, S] + qkv_f)
+    H = allocf(eng, images * T, 384)
+    run(eng, K_LN, [images * T], [X, up(eng, gamma), up(eng, beta), H])
+    run(eng, K_QKV, [images, grid, tpad], [H, upf(eng, f16(w)), up(eng, b), C, S] + qkv_u)
+    h = oracle.layernorm(x.astype(np.float64), gamma, beta)
+    to_tok = lambda a, i: a[i, :, :T].transpose(1, 0, 2).reshape(T, 384)
+    for part, lo in (("q", 0), ("v", 768)):
+        idx = 0 if part == "q" else 2
+        gf = eng.read(qkv_f[idx], np.float16, (images, 6, tpad, 64))
+        gu = eng.read(qkv_u[idx], np.float16, (images, 6, tpad, 64))
+        for i in range(images):
+            ref = oracle.linear(h[i * T:(i + 1) * T], w[lo:lo + 384].astype(np.float64), b[lo:lo + 384])
+            if part == "q":
+                ref = oracle.rope(ref, grid)
+            ef = np.abs(to_tok(gf, i).astype(np.float64) - ref).max()
+            eu = np.abs(to_tok(gu, i).astype(np.float64) - ref).max()
+            print(f"{case} {part} img {i} max_abs vs oracle: folded {ef:.3g}, unfused {eu:.3g}")
+            assert ef <= max(1.25 * eu, 3e-3 + 2.0**-10 * np.abs(ref).max())
+
+
+@pytest.mark.parametrize("case", ["offset", "outlier", "both"])
+def test_swiglu_layernorm_fused_adversarial(eng, case):
+    rng = np.random.default_rng({"offset": 4, "outlier": 5, "both": 6}[case])
+    rows = 1001
+    x = adversarial_rows(rng, rows, case)
+    gamma = (1 + rng.normal(size=384) * 0.2).astype(np.float32)
+    beta = (rng.normal(size=384) * 0.2).astype(np.float32)
+    wg, wu = (rng.normal(size=(1536, 384)) * 0.05).astype(np.float32), (rng.normal(size=(1536, 384)) * 0.05).astype(np.float32)
+    bg, bu = (rng.normal(size=1536) * 0.2).astype(np.float32), (rng.normal(size=1536) * 0.2).astype(np.float32)
+    w, b = pack_gateup(wg, wu, bg, bu)
+    wl, wsum, t = fold(w, b, gamma, beta)
+    X = upf(eng, x)
+    act_f, act_u, H = allocf(eng, rows, 1536), allocf(eng, rows, 1536), allocf(eng, rows, 384)
+    run(eng, K_SWIGLU_LN, [rows], [X, up(eng, slot_stats(x)), upf(eng, wl), up(eng, wsum), up(eng, t), act_f])
+    run(eng, K_LN, [rows], [X, up(eng, gamma), up(eng, beta), H])
+    run(eng, K_SWIGLU, [rows], [H, upf(eng, f16(w)), up(eng, b), act_u])
+    h = oracle.layernorm(x.astype(np.float64), gamma, beta)
+    gpre, upre = oracle.linear(h, wg.astype(np.float64), bg), oracle.linear(h, wu.astype(np.float64), bu)
+    ref = oracle.swiglu(gpre, upre)
+    gf, gu = readf(eng, act_f, rows, 1536).astype(np.float64), readf(eng, act_u, rows, 1536).astype(np.float64)
+    ef, eu = np.abs(gf - ref).max(), np.abs(gu - ref).max()
+    # First-order bound: both plans round the GEMM operands to f16 (W' or W,
+    # and h in the unfused plan), so each pre-activation is off by at most
+    # 2^-10 sum_k |h_k w_k| (+ a floor); silu(g) u carries those errors as
+    # |silu(g)| du + |u silu'(g)| dg, then rounds to f16.
+    sig = 1 / (1 + np.exp(-gpre))
+    dg = 2.0**-10 * (np.abs(h) @ np.abs(wg.T)) + 1e-4
+    du = 2.0**-10 * (np.abs(h) @ np.abs(wu.T)) + 1e-4
+    bound = 2.0**-10 * np.abs(ref) + np.abs(gpre * sig) * du + np.abs(upre * sig * (1 + gpre * (1 - sig))) * dg + 1e-4
+    for name, got in (("folded", gf), ("unfused", gu)):
+        slack = (np.abs(got - ref) / bound).max()
+        print(f"{case} swiglu {name}: max error / first-order bound {slack:.3f}")
+        assert slack <= 1.0, name
+    # The unfused GEMM against the oracle on the GPU's own f16 h: the error
+    # of the GEMM alone, with LayerNorm and the h rounding taken out.
+    hd = readf(eng, H, rows, 384).astype(np.float64)
+    wd = f16(w).astype(np.float64)
+    gemm = oracle.swiglu(oracle.linear(hd, wd[np.arange(3072) % 64 < 32], b[np.arange(3072) % 64 < 32]),
+                         oracle.linear(hd, wd[np.arange(3072) % 64 >= 32], b[np.arange(3072) % 64 >= 32]))
+    eg = np.abs(gu - gemm).max()
+    print(f"{case} swiglu max_abs vs oracle: folded {ef:.3g}, unfused {eu:.3g}; unfused GEMM on its own h {eg:.3g}")
+    assert ef <= max(1.25 * eu, 3e-3 + 2.0**-10 * np.abs(ref).max())
+
+
+def test_stats_producer_adversarial_rows(eng):
+    # The producers' slot statistics (two-pass per 64-column slot, combined
+    # by the consumers) on the same adversarial rows: K_RESID_S with a zero
+    # weight leaves x unchanged and writes the statistics of x.
+    rng = np.random.default_rng(8)
+    rows = 1001
+    x0 = adversarial_rows(rng, rows, "both")
+    x, st = upf(eng, x0), eng.allocate(rows * 48)
+    zeros = np.zeros(384, np.float32)
+    run(eng, K_RESID_S, [rows, 384], [upf(eng, np.zeros((rows, 384), np.float16)),
+                                      upf(eng, np.zeros((384, 384), np.float16)), up(eng, zeros), up(eng, zeros), x, st])
+    assert np.array_equal(readf(eng, x, rows, 384), x0)
+    check_stats(eng.read(st, np.float32, (rows, 12)), x0, "adversarial stats")
+
+
+# ---------------------------------------------------------------------------
+# Bitwise repeatability of the DMA-fed kernels at the shapes the bench runs:
+# batch 64 and 32 at 224x224 and batch 8 at 512x512. The GEMMs move their
+# weight stages, and attention its K/V blocks, into LDS with DMA loads;
+# waiting for one correctly depends on the order in which those loads and
+# the register loads complete, and a wrong wait shows up as results that
+# change from launch to launch (stale data in LDS), not as a fault.
+
+SHAPES = {"b64": (64, 14), "b32": (32, 14), "512b8": (8, 32)}
+
+
+@pytest.mark.parametrize("shape", list(SHAPES))
 @pytest.mark.parametrize("kernel", ["qkv_ln", "swiglu_ln", "resid_384", "resid_1536", "splitk"])
-def test_gemm_bitwise_repeatable(eng, kernel):
+def test_gemm_bitwise_repeatable(eng, kernel, shape):
     rng = np.random.default_rng(5)
-    images, grid = 64, 14
+    images, grid = SHAPES[shape]
     T = grid * grid + 5
     tpad = (T + 127) // 128 * 128
     M = images * T
@@ -538,3 +663,64 @@ def test_gemm_bitwise_repeatable(eng, kernel):
     for rep in range(4):
         again = once()
         assert np.array_equal(first, again), f"{kernel}: launch {rep + 2} differs in {int((first != again).sum())} elements"
+
+
+@pytest.mark.parametrize("shape", ["b64", "512b8"])
+def test_attention_bitwise_repeatable(eng, shape):
+    # T = 201 runs the unrolled 32-key-block loop, T = 1029 the run-time
+    # 64-key-block loop; both DMA K/V two blocks ahead into three buffers.
+    images, grid = SHAPES[shape]
+    rng = np.random.default_rng(12)
+    T = grid * grid + 5
+    tpad = (T + 127) // 128 * 128
+    ins = [up(eng, head_major(f16(rng.normal(size=(images * T, 384)) * s), images, T, tpad)) for s in (2.0, 1.0, 1.0)]
+
+    def once():
+        out = allocf(eng, images * T, 384)
+        run(eng, K_ATTN, [images, grid, tpad], ins + [out])
+        return readf(eng, out, images * T, 384)
+
+    first = once()
+    assert np.all(np.isfinite(first))
+    for rep in range(4):
+        again = once()
+        assert np.array_equal(first, again), f"attention {shape}: launch {rep + 2} differs in {int((first != again).sum())} elements"
+
+
+@pytest.mark.parametrize("case", ["uniform", "outlier"])
+def test_mfma_accumulation_mixed_magnitudes(eng, case):
+    # The f32 split-K slabs give a GEMM's f32 accumulator with no f16 output
+    # rounding: against the exact float64 product of the same f16 operands,
+    # the error measures the MFMA accumulation alone. 'outlier' rows hold
+    # 2-4 channels at +-200 among N(0, 1) ones (products ~200x apart within
+    # one 16-deep MFMA step); 'uniform' rows are N(0, 1). The error is stated
+    # relative to the row's largest |a_k w_k| and to sum_k |a_k w_k|.
+    rng = np.random.default_rng(31)
+    rows, kdim, splits = 1001, 1536, 4
+    a = rng.normal(size=(rows, kdim))
+    if case == "outlier":
+        for r in range(rows):
+            ch = rng.choice(kdim, size=rng.integers(2, 5), replace=False)
+            a[r, ch] = rng.choice([-200.0, 200.0], size=ch.size)
+    a = f16(a)
+    w = f16(rng.normal(size=(384, kdim)) * 0.05)
+    part = eng.allocate(splits * rows * 384 * 4)
+    run(eng, K_SPLITK, [rows, kdim, splits], [upf(eng, a), upf(eng, w), part])
+    p = eng.read(part, np.float32, (splits, rows, 384)).astype(np.float64)
+    ad, wd = a.astype(np.float64), w.astype(np.float64)
+    c = kdim // splits
+    worst_max, worst_sum = 0.0, 0.0
+    for s in range(splits):
+        sl = slice(s * c, (s + 1) * c)
+        exact = ad[:, sl] @ wd[:, sl].T
+        mag = np.abs(ad[:, sl]) @ np.abs(wd[:, sl]).T
+        big = np.stack([np.abs(ad[:, sl] * wd[n, sl]).max(1) for n in range(384)], 1)
+        err = np.abs(p[s] - exact)
+        worst_max = max(worst_max, float((err / big).max()))
+        worst_sum = max(worst_sum, float((err / mag).max()))
+    print(f"{case}: MFMA accumulation error <= {worst_max:.3g} x max|a w|, {worst_sum:.3g} x sum|a w| "
+          f"(2^{np.log2(worst_max):.1f}, 2^{np.log2(worst_sum):.1f})")
+    # measured on the MI355X: <= 2^-17 x max|a w| and <= 2^-21 x sum|a w| with
+    # or without outliers, i.e. products are not truncated to the largest
+    # one's exponent; the bar leaves 8x margin.
+    assert worst_max < 2.0**-14 and worst_sum < 2.0**-18

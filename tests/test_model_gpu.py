@@ -128,6 +128,97 @@ def test_full_batch_64_rows_independent_of_batch(models, oracle_weights):
         assert c_all > 0.9999 and c_cls > 0.9999
 
 
+def test_batch_32_stress_matches_oracle(models, oracle_weights):
+    # Config 2: the reference's default resident capacity (lib.rs:20-27),
+    # b = 32 (6,432 token rows, three image groups of 10-11 images), on the
+    # stress preset; images from the first, middle and last group against the
+    # oracle, and the batch's first and last images bitwise equal to the same
+    # images run as a batch of 2.
+    m = models(1, max_batch=32)
+    px = d.random_pixels(21, 32)
+    out = m.forward(px)
+    assert out.shape == (32, 201, 384) and np.all(np.isfinite(out))
+    for i in (0, 15, 31):
+        c_all, c_cls, _ = compare(out[i], oracle.forward(oracle_weights(1), px[i], 14), f"b32 stress image {i}")
+        assert c_all > 0.9999 and c_cls > 0.9999
+    assert np.array_equal(out[:2], m.forward(px[:2]))
+    assert np.array_equal(out[30:], m.forward(px[30:]))
+
+
+def test_batch_64_stress_every_grouping(models, oracle_weights):
+    # Config 3 (the headline, b = 64) on the stress preset: one image of each
+    # of the three default image groups (and the last image) against the
+    # oracle; all 64 outputs bitwise equal for every grouping bench.py may
+    # pick (1-4 concurrent groups) and to the same images run as batches of 16.
+    m = models(1, max_batch=64)
+    px = d.random_pixels(22, 64)
+    m.set_branches(3)
+    out = m.forward(px)
+    assert out.shape == (64, 201, 384) and np.all(np.isfinite(out))
+    for i in (0, 21, 42, 63):
+        c_all, c_cls, _ = compare(out[i], oracle.forward(oracle_weights(1), px[i], 14), f"b64 stress image {i}")
+        assert c_all > 0.9999 and c_cls > 0.9999
+    try:
+        for n in (1, 2, 4):
+            m.set_branches(n)
+            assert np.array_equal(m.forward(px), out), f"{n} groups"
+    finally:
+        m.set_branches(3)
+    for first in range(0, 64, 16):
+        assert np.array_equal(m.forward(px[first:first + 16]), out[first:first + 16]), first
+
+
+def test_512_batch_8_grouped_plan(models, oracle_weights):
+    # Config 5 as bench.py runs it: 512x512 (1029 tokens), b = 8 in two
+    # concurrent image groups of 4. One image per group against the oracle;
+    # the batch bitwise equal to one group and to batches of 2 (a batch of 1
+    # takes the split-K down projection, lib.rs:218-225, so it is not
+    # bitwise the same).
+    m = models(1, max_batch=8, image_size=512)
+    px = d.random_pixels(23, 8, 512)
+    out = m.forward(px)
+    assert out.shape == (8, 1029, 384) and np.all(np.isfinite(out))
+    for i in (0, 7):
+        c_all, c_cls, _ = compare(out[i], oracle.forward(oracle_weights(1), px[i], 32), f"512 b8 image {i}")
+        assert c_all > 0.9999 and c_cls > 0.9999
+    try:
+        m.set_branches(1)
+        assert np.array_equal(m.forward(px), out)
+    finally:
+        m.set_branches(3)
+    assert np.array_equal(m.forward(px[:2]), out[:2])
+    assert np.array_equal(m.forward(px[6:]), out[6:])
+
+
+@pytest.mark.parametrize("dtype", ["F16", "BF16"])
+def test_half_precision_checkpoints(models, tmp_path, weight_file, dtype):
+    # weights.rs:30-45: F16 and BF16 tensors are widened to float32 before
+    # packing. The stress weights stored as F16 / BF16 must give (a) the
+    # oracle's forward on the widened values and (b) bitwise the forward of
+    # an F32 file holding those widened values (widening is exact, so the
+    # packed bytes are the same).
+    import torch
+    from safetensors.numpy import load_file, save_file
+    from safetensors.torch import save_file as save_torch
+
+    src = load_file(weight_file(1))
+    tdt = torch.float16 if dtype == "F16" else torch.bfloat16
+    half = {k: torch.from_numpy(v).to(tdt) for k, v in src.items()}
+    widened = {k: v.to(torch.float32).numpy() for k, v in half.items()}
+    assert any(not np.array_equal(widened[k], src[k]) for k in src)  # the rounding is real
+    hpath, fpath = str(tmp_path / "half.safetensors"), str(tmp_path / "widened.safetensors")
+    save_torch(half, hpath)
+    save_file(widened, fpath)
+    px = d.random_pixels(24, 2)
+    with d.DINOv3.load(hpath, d.Options(0, 2)) as mh, d.DINOv3.load(fpath, d.Options(0, 2)) as mf:
+        got = mh.forward(px)
+        assert np.array_equal(got, mf.forward(px))
+    ow = oracle.Weights(widened)
+    for i in range(2):
+        c_all, c_cls, _ = compare(got[i], oracle.forward(ow, px[i], 14), f"{dtype} checkpoint image {i}")
+        assert c_all > 0.9999 and c_cls > 0.9999
+
+
 @pytest.mark.parametrize("preset", [0, 1])
 def test_layernorm_fusion_matches_unfused_plan(models, oracle_weights, preset):
     m = models(preset, max_batch=8)
