@@ -82,9 +82,10 @@ def timed_replays(model, b, steps):
     return (time.perf_counter() - t0) / steps
 
 
-def replay_latency(model, b, samples):
-    """Median host-clock time of one synchronised replay (the reference's
-    ForwardTimings scope, engine.rs:130-190)."""
+def replay_distribution(model, b, samples):
+    """Host-clock times of synchronised replays, the reference's
+    ForwardTimings scope and statistics (engine.rs:130-190): median =
+    t[n/2], p95 = t[ceil(0.95 n) - 1] of the sorted samples, in seconds."""
     t = []
     for _ in range(samples):
         model.synchronize()
@@ -92,7 +93,24 @@ def replay_latency(model, b, samples):
         model.replay(b)
         model.synchronize()
         t.append(time.perf_counter() - t0)
-    return sorted(t)[len(t) // 2]
+    t.sort()
+    return t[len(t) // 2], t[-(-95 * len(t) // 100) - 1]
+
+
+def sync_stats(model, b, samples):
+    med, p95 = replay_distribution(model, b, samples)
+    return {"median_ms": round(med * 1e3, 4), "p95_ms": round(p95 * 1e3, 4), "samples": samples,
+            "images_per_s_at_median": round(b / med, 1)}
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def cpu_baseline(path, seconds):
@@ -119,7 +137,7 @@ def cpu_baseline(path, seconds):
     n, dt = run(1, seconds)
     cores = min(16, len(os.sched_getaffinity(0)))
     nm, dtm = run(cores, seconds / 3)
-    return {"value": round(n / dt, 4), "unit": "images/s", "cores": 1, "kind": "port",
+    return {"value": round(n / dt, 4), "unit": "images/s", "cores": 1, "kind": "port", "cpu": cpu_model(),
             "sample": f"{n} image(s) of the b=64 workload at 224x224 through the float64 C oracle "
                       f"(oracle/dinov3_oracle.c), 1 thread, {dt:.1f} s",
             "all_cores": {"value": round(nm / dtm, 4), "cores": cores,
@@ -208,6 +226,7 @@ def main():
             model.replay(b)
         sec = timed_replays(model, b, args.steps)
         value = b / sec
+        sync = sync_stats(model, b, max(100, args.steps))
 
         # Batch 32 (config 2) on the same resident model, with its own short
         # trial of the image grouping.
@@ -223,6 +242,7 @@ def main():
         for _ in range(args.warmup):
             model.replay(32)
         sec32 = timed_replays(model, 32, args.steps)
+        sync32 = sync_stats(model, 32, max(100, args.steps))
         model.set_branches(branches)
 
         # Batch 1 (the reference's own benchmark case: graph-replay latency of
@@ -230,7 +250,7 @@ def main():
         model.stage(px[:1])
         for _ in range(args.warmup):
             model.replay(1)
-        sec1 = replay_latency(model, 1, args.steps)
+        sec1, p95_1 = replay_distribution(model, 1, max(100, args.steps))
 
         # End to end through the host API (PCIe-inclusive; never `value`):
         # forward() of 4 chunks of b images from host memory to host memory,
@@ -313,11 +333,13 @@ def main():
                    "down_proj": "splitk" if mode == 1 else "resid", "branches": branches,
                    "weights": "seeded random init (BASELINE)"},
         "mfma_frac_forward": round(value * GFLOP_PER_IMAGE / 1e3 / PEAK_TFLOPS, 4),
-        "batch32": {"value": round(32 / sec32, 1), "ms_per_step": round(sec32 * 1e3, 4), "branches": branches32},
-        "batch1": {"value": round(1 / sec1, 1), "ms_per_step": round(sec1 * 1e3, 4),
+        "sync_replay": sync,
+        "batch32": {"value": round(32 / sec32, 1), "ms_per_step": round(sec32 * 1e3, 4), "branches": branches32,
+                    "sync_replay": sync32},
+        "batch1": {"value": round(1 / sec1, 1), "ms_per_step": round(sec1 * 1e3, 4), "p95_ms": round(p95_1 * 1e3, 4),
                    "what": "median synchronised graph-replay latency of one image (the reference's b = 1 case)"},
         "highres_512_b8": {"value": round(8 / sec_hr, 1), "unit": "images/s", "ms_per_step": round(sec_hr * 1e3, 4),
-                           "branches": branches_hr, "what": "BASELINE.json config 4: 512x512, 1029 tokens, batch 8"},
+                           "branches": branches_hr, "what": "BASELINE.json config 5: 512x512, 1029 tokens, batch 8"},
         "end_to_end": {"value": round(e2e_rate, 1), "unit": "images/s",
                        "what": f"forward() of {4 * b} images from host memory to host memory (PCIe and host copies "
                                f"included, chunks of {b} pipelined); not the metric"},

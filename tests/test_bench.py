@@ -87,3 +87,29 @@ def test_bench_json_line(gpu):
     assert abs(roof["achieved"] - work / (roof["avg_us"] * 1e-6)) <= 0.01 * roof["achieved"]
     cpu = d["cpu_baseline"]
     assert cpu["kind"] == "port" and cpu["cores"] == 1 and cpu["value"] > 0 and cpu["sample"]
+
+
+def test_sync_replay_statistics(monkeypatch):
+    # engine.rs:130-190: median = t[n/2], p95 = t[ceil(0.95 n) - 1] of the
+    # sorted samples. Replays of 1..100 ms in shuffled order.
+    import random
+
+    order = list(range(1, 101))
+    random.Random(4).shuffle(order)
+    clock = []
+    for ms in order:
+        clock += [0.0, ms / 1e3]
+    it = iter(clock)
+    monkeypatch.setattr(bench.time, "perf_counter", lambda: next(it))
+
+    class Fake:
+        def synchronize(self):
+            pass
+
+        def replay(self, b):
+            pass
+
+    s = bench.sync_stats(Fake(), 64, 100)
+    assert s["median_ms"] == 51.0 and s["p95_ms"] == 95.0 and s["samples"] == 100
+    assert s["images_per_s_at_median"] == round(64 / 0.051, 1)
+    assert bench.cpu_model()
