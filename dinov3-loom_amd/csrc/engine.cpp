@@ -15,6 +15,7 @@
 #include <vector>
 
 #include "../../include/dinov3_engine.h"
+#include "engine_internal.hpp"
 #include "errors.hpp"
 #include "kernels/launch.hpp"
 
@@ -41,6 +42,7 @@ struct dhx_engine {
     std::vector<hipEvent_t> join;
     std::vector<void*> buffers;
     std::vector<uint64_t> sizes;
+    std::vector<char> owned;  // 0: an external slot (engine_external), never freed here
     std::map<uint64_t, Recorded> graphs;
     void* readback = nullptr;
     uint64_t readback_bytes = 0;
@@ -340,6 +342,38 @@ void check_slot(const dhx_engine* e, uint32_t slot) {
 
 }  // namespace
 
+namespace dhx {
+
+uint32_t engine_external(dhx_engine* e, void* ptr, uint64_t bytes) {
+    e->buffers.push_back(ptr);
+    e->sizes.push_back(bytes);
+    e->owned.push_back(0);
+    return (uint32_t)(e->buffers.size() - 1);
+}
+
+void engine_rebind(dhx_engine* e, uint32_t buffer, void* ptr, uint64_t bytes) {
+    if (buffer >= e->buffers.size() || e->owned[buffer]) throw Error("not an external buffer slot");
+    e->buffers[buffer] = ptr;
+    e->sizes[buffer] = bytes;
+}
+
+void engine_queue(dhx_engine* e, const dhx_launch* launches, size_t n, hipStream_t stream) {
+    ensure_usable(e);
+    for (size_t i = 0; i < n; ++i) validate(e, launches[i]);
+    set_device(e);
+    for (size_t i = 0; i < n; ++i) hip_check(e, launch_one(e, launches[i], stream), "kernel launch");
+}
+
+hipStream_t engine_stream(const dhx_engine* e) { return e->stream; }
+
+int engine_device(const dhx_engine* e) { return e->device; }
+
+void engine_check(dhx_engine* e, hipError_t err, const char* what) { hip_check(e, err, what); }
+
+void engine_ensure_usable(const dhx_engine* e) { ensure_usable(e); }
+
+}  // namespace dhx
+
 extern "C" {
 
 int dhx_engine_open(int32_t device, dhx_engine** out) {
@@ -378,7 +412,8 @@ void dhx_engine_free(dhx_engine* e) {
     release_staging(e);  // waits for the transfer streams before their buffers go
     for (auto& kv : e->graphs)
         if (kv.second.exec) (void)hipGraphExecDestroy(kv.second.exec);
-    for (void* b : e->buffers) (void)hipFree(b);
+    for (size_t i = 0; i < e->buffers.size(); ++i)
+        if (e->owned[i]) (void)hipFree(e->buffers[i]);
     if (e->readback) (void)hipHostFree(e->readback);
     for (hipStream_t s : e->aux) {
         (void)hipStreamSynchronize(s);
@@ -401,6 +436,7 @@ int dhx_allocate(dhx_engine* e, uint64_t bytes, dhx_region* out) {
         hip_check(e, hipMalloc(&p, std::max<uint64_t>(bytes, 16)), "hipMalloc");
         e->buffers.push_back(p);
         e->sizes.push_back(bytes);
+        e->owned.push_back(1);
         // Zero once: padded rows of q/k/v are never written and must stay finite.
         // The engine's stream does not synchronise with the legacy default
         // stream, so the fill is queued on it and waited for: a later upload or

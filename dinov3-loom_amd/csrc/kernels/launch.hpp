@@ -136,7 +136,22 @@ struct ReduceArgs {
     float* stats = nullptr;  // optional: row statistics of the updated x
 };
 
+// Rows tokens .. tpad-1 of q, k and v [images][6][tpad][64] set to zero:
+// attention reads them as masked keys, so they must be finite. For buffers
+// that did not come zeroed from the engine (the allocation-free forward's
+// scratch, which keeps earlier calls' data). A fill kernel, not a memset, so
+// that the launch can be captured into a graph.
+struct PadRowsArgs {
+    half_t* q;
+    half_t* k;
+    half_t* v;
+    int images;
+    int tokens;
+    int tpad;
+};
+
 hipError_t launch_layernorm(const LayerNormArgs& a, hipStream_t s);
+hipError_t launch_zero_pad_rows(const PadRowsArgs& a, hipStream_t s);
 hipError_t launch_patch_embed(const PatchEmbedArgs& a, hipStream_t s);
 hipError_t launch_qkv_rope(const QkvArgs& a, hipStream_t s);
 hipError_t launch_attention(const AttentionArgs& a, hipStream_t s);

@@ -137,7 +137,29 @@ __global__ __launch_bounds__(kThreads) void splitk_reduce_kernel(ReduceArgs p) {
     }
 }
 
+// One thread per 16-byte piece of a padding row (8 per 64-channel row) of
+// each (tensor, image, head).
+__global__ __launch_bounds__(kThreads) void zero_pad_rows_kernel(PadRowsArgs p) {
+    const int pad = p.tpad - p.tokens;
+    const size_t per_tensor = (size_t)p.images * kHeads * pad * 8;
+    const size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= 3 * per_tensor) return;
+    const int t = (int)(i / per_tensor);
+    const size_t j = i - t * per_tensor;
+    const size_t ih = j / ((size_t)pad * 8);  // image * heads + head
+    const int row = p.tokens + (int)(j / 8 % pad), piece = (int)(j % 8);
+    half_t* const base = t == 0 ? p.q : t == 1 ? p.k : p.v;
+    *(half8_t*)(base + (ih * p.tpad + row) * kHeadDim + piece * 8) = half8_t{};
+}
+
 }  // namespace
+
+hipError_t launch_zero_pad_rows(const PadRowsArgs& a, hipStream_t s) {
+    const size_t n = 3ull * a.images * kHeads * (a.tpad - a.tokens) * 8;
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(zero_pad_rows_kernel, dim3((unsigned)((n + kThreads - 1) / kThreads)), dim3(kThreads), 0, s, a);
+    return hipGetLastError();
+}
 
 hipError_t launch_layernorm(const LayerNormArgs& a, hipStream_t s) {
     hipLaunchKernelGGL(layernorm_kernel, dim3((a.rows + 31) / 32), dim3(kThreads), 0, s, a);

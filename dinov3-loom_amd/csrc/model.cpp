@@ -2,18 +2,23 @@
 // load / from_pretrained / forward / cls / patch_mean / benchmark, batch
 // chunking, the buffer plan and the per-batch launch plan (`prepare`),
 // built on the engine C ABI exactly as lib.rs builds on HRX.
+#include <hip/hip_runtime.h>
+
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
 #include <map>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <sys/stat.h>
 #include <thread>
 #include <vector>
 
 #include "../../include/dinov3.h"
+#include "engine_internal.hpp"
 #include "errors.hpp"
+#include "kernels/launch.hpp"
 #include "weights.hpp"
 
 namespace dhx {
@@ -71,6 +76,34 @@ std::string hub_weights() {
 void check(int rc, dhx_engine* e) {
     if (rc != 0) throw Error(dhx_last_error(e));
 }
+
+// The allocation-free forward's intermediate buffers: one array per GPU,
+// loaded with the library's code object and held until the process ends.
+// Host code never uses the name as an address (on the host it is only a
+// handle for the symbol lookup): scratch_address() asks the runtime for
+// each device's copy once, with that device current.
+constexpr uint64_t kScratchBytes = DINOV3_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch[kMaxDevices] = {};
+
+void* scratch_address(int device) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (device < 0 || device >= kMaxDevices) throw Error("device id out of range for the scratch table");
+    if (!g_scratch[device]) {
+        hipError_t err = hipSetDevice(device);
+        void* p = nullptr;
+        if (err == hipSuccess) err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (err != hipSuccess || !p)
+            throw Error(std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(err));
+        g_scratch[device] = p;
+    }
+    return g_scratch[device];
+}
+
+constexpr uint64_t align256(uint64_t v) { return (v + 255) & ~255ull; }
 
 // Finite check of the whole input before any GPU work (lib.rs validates
 // every pixel first), split over host threads for large batches.
@@ -133,6 +166,17 @@ public:
                                           r * kHiddenU * 4, B * image_elems_ * 4};
         for (int i = 0; i < kBuffers; ++i) check(dhx_allocate(e, sizes[i], &a_[i]), e);
         check(dhx_reserve_staging(e, B * image_elems_ * 4, r * kHiddenU * 4), e);
+        // The allocation-free forward: this device's scratch array and three
+        // external buffer slots (scratch, caller input, caller output). A
+        // failed lookup only disables that entry point (it reports why).
+        try {
+            ext_scratch_ = dhx::engine_external(e, scratch_address(opts.device), kScratchBytes);
+            ext_in_ = dhx::engine_external(e, nullptr, 0);
+            ext_out_ = dhx::engine_external(e, nullptr, 0);
+            noalloc_launches_.reserve(128);
+        } catch (const Error& ex) {
+            noalloc_error_ = ex.what();
+        }
     }
 
     dhx_engine* engine() { return engine_.get(); }
@@ -231,7 +275,7 @@ public:
         for (uint32_t g = 0; g < nb; ++g) {
             const uint64_t first = b * g / nb, end = b * (g + 1) / nb;
             const size_t before = l.size();
-            plan(first, end - first, b, slot, frag_row0, l);
+            plan(first, end - first, b, slot, frag_row0, l, a_);
             counts.push_back(l.size() - before);
             frag_row0 += ((end - first) * tokens_ + 31) / 32 * 32;
         }
@@ -239,8 +283,8 @@ public:
     }
 
     // The launches for images [first, first + n) of a batch of b.
-    void plan(uint64_t first, uint64_t n, uint64_t b, uint32_t slot, uint64_t frag_row0,
-              std::vector<dhx_launch>& l) const {
+    void plan(uint64_t first, uint64_t n, uint64_t b, uint32_t slot, uint64_t frag_row0, std::vector<dhx_launch>& l,
+              const dhx_region* bufs) const {
         const uint32_t r = (uint32_t)(n * tokens_);
         const uint32_t B = (uint32_t)n, G = grid_, TP = (uint32_t)tpad_;
         auto add = [&](uint32_t kernel, std::initializer_list<uint32_t> s, std::initializer_list<dhx_region> bind) {
@@ -255,14 +299,14 @@ public:
         auto w = [&](const std::string& name) { return weights_.at(name); };
         // This group's slice of a buffer holding `per_image` bytes per image.
         auto part = [&](int buf, uint64_t per_image) {
-            dhx_region g = a_[buf];
+            dhx_region g = bufs[buf];
             g.offset += first * per_image;
             g.bytes = n * per_image;
             return g;
         };
         // This group's rows of a fragment-order activation buffer of width k.
         auto frag_part = [&](int buf, uint64_t k) {
-            dhx_region g = a_[buf];
+            dhx_region g = bufs[buf];
             g.offset += frag_row0 * k * 2;
             g.bytes = (n * tokens_ + 31) / 32 * 32 * k * 2;
             return g;
@@ -321,6 +365,59 @@ public:
         add(DHX_K_LAYERNORM_F32, {r}, {X, w("norm_w"), w("norm_b"), O});
     }
 
+    // dinov3_forward_noalloc: the plan of one image group over the scratch
+    // array (laid out for this batch, 256-byte aligned pieces) and the
+    // caller's device input and output, queued on `stream` after a fill of
+    // the q/k/v padding rows. The same launches and arithmetic per row as
+    // forward(), so the same bits. Allocates nothing and does not wait.
+    void forward_noalloc(const float* pixels, uint64_t images, float* out, hipStream_t stream) {
+        dhx_engine* e = engine_.get();
+        dhx::engine_ensure_usable(e);
+        if (!noalloc_error_.empty()) throw Error("the allocation-free forward is unavailable: " + noalloc_error_);
+        if (images == 0) return;
+        if (!pixels || !out) throw Error("null device pointer");
+        if ((reinterpret_cast<uintptr_t>(pixels) | reinterpret_cast<uintptr_t>(out)) % 16 != 0)
+            throw Error("device input and output must be 16-byte aligned");
+        if (images > 64) throw Error("the allocation-free forward takes at most 64 images per call");
+        const uint64_t r = images * tokens_, rf = (r + 31) / 32 * 32;
+        const uint64_t heads = images * 6 * tpad_ * 64 * 2;
+        const bool split = images == 1 || splitk_ == 1;
+        uint64_t need[kBuffers] = {};
+        need[kX] = rf * kHiddenU * 2;
+        need[kH] = fused_ln_ ? 0 : rf * kHiddenU * 2;
+        need[kQ] = need[kK] = need[kV] = heads;
+        need[kAttn] = rf * kHiddenU * 2;
+        need[kAct] = rf * 1536 * 2;
+        need[kStats] = fused_ln_ ? r * 12 * 4 : 0;
+        need[kPartials] = split ? (uint64_t)kSplits * r * kHiddenU * 4 : 0;
+        dhx_region bufs[kBuffers] = {};
+        uint64_t at = 0;
+        for (int i = 0; i < kBuffers; ++i) {
+            if (i == kOut || i == kOut1 || i == kImage || i == kImage1) continue;
+            bufs[i] = dhx_region{ext_scratch_, at, need[i]};
+            at += align256(need[i]);
+        }
+        if (at > kScratchBytes)
+            throw Error("the allocation-free forward of " + std::to_string(images) + " images needs " +
+                        std::to_string(at) + " bytes of scratch, more than its " + std::to_string(kScratchBytes));
+        const uint64_t in_bytes = images * image_elems_ * 4, out_bytes = r * kHiddenU * 4;
+        dhx::engine_rebind(e, ext_in_, const_cast<float*>(pixels), in_bytes);
+        dhx::engine_rebind(e, ext_out_, out, out_bytes);
+        bufs[kImage] = bufs[kImage1] = dhx_region{ext_in_, 0, in_bytes};
+        bufs[kOut] = bufs[kOut1] = dhx_region{ext_out_, 0, out_bytes};
+        noalloc_launches_.clear();  // capacity reserved at load: no reallocation
+        plan(0, images, images, 0, 0, noalloc_launches_, bufs);
+        char* const base = static_cast<char*>(scratch_address(dhx::engine_device(e)));
+        const dhx::PadRowsArgs pad{reinterpret_cast<dhx::half_t*>(base + bufs[kQ].offset),
+                                   reinterpret_cast<dhx::half_t*>(base + bufs[kK].offset),
+                                   reinterpret_cast<dhx::half_t*>(base + bufs[kV].offset), (int)images, (int)tokens_,
+                                   (int)tpad_};
+        if (!stream) stream = dhx::engine_stream(e);
+        dhx::engine_check(e, hipSetDevice(dhx::engine_device(e)), "hipSetDevice");
+        dhx::engine_check(e, dhx::launch_zero_pad_rows(pad, stream), "kernel launch");
+        dhx::engine_queue(e, noalloc_launches_.data(), noalloc_launches_.size(), stream);
+    }
+
     // Number of image groups run side by side for a batch of b.
     uint32_t groups(uint64_t b) const {
         return (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(branches_, b / kMinBranchImages));
@@ -350,6 +447,9 @@ private:
     std::unique_ptr<dhx_engine, EngineFree> engine_;
     std::map<std::string, dhx_region> weights_;
     dhx_region a_[kBuffers];
+    uint32_t ext_scratch_ = 0, ext_in_ = 0, ext_out_ = 0;
+    std::vector<dhx_launch> noalloc_launches_;
+    std::string noalloc_error_;
 };
 
 }  // namespace dhx
@@ -426,6 +526,10 @@ int dinov3_hub_weights(char* path_out, uint64_t capacity) {
 
 int dinov3_forward(dinov3_model* m, const float* pixels, uint64_t n, float* out, uint64_t out_floats) {
     return guarded(m, [&](dhx::Model& x) { x.forward(pixels, n, out, out_floats); });
+}
+
+int dinov3_forward_noalloc(dinov3_model* m, const float* pixels, uint64_t images, float* out, void* stream) {
+    return guarded(m, [&](dhx::Model& x) { x.forward_noalloc(pixels, images, out, static_cast<hipStream_t>(stream)); });
 }
 
 int dinov3_cls(dinov3_model* m, const float* pixels, uint64_t n, float* out, uint64_t out_floats) {

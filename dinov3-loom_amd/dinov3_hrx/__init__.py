@@ -83,6 +83,7 @@ def _load_library() -> ctypes.CDLL:
     for name in ("dinov3_forward", "dinov3_cls", "dinov3_patch_mean"):
         getattr(L, name).argtypes = [vp, fp, c.c_uint64, fp, c.c_uint64]
     L.dinov3_benchmark.argtypes = [vp, fp, c.c_uint64, c.c_uint64, c.POINTER(_Timings)]
+    L.dinov3_forward_noalloc.argtypes = [vp, vp, c.c_uint64, vp, vp]
     L.dinov3_free.argtypes = [vp]
     L.dinov3_image_elements.argtypes = [vp]
     L.dinov3_image_elements.restype = c.c_uint64
@@ -221,6 +222,13 @@ class DINOv3:
 
     def _pixels(self, pixels) -> np.ndarray:
         return np.ascontiguousarray(pixels, dtype=np.float32).reshape(-1)
+
+    def forward_noalloc(self, d_pixels: int, images: int, d_out: int, stream: int = 0) -> None:
+        """dinov3_forward_noalloc: device addresses in and out (images x 3 x S
+        x S and images x T x 384 float32), launches queued on `stream` (a
+        hipStream_t, 0 = the model's own) without waiting; no allocation."""
+        _check(_lib.dinov3_forward_noalloc(self._h, ctypes.c_void_p(d_pixels), images, ctypes.c_void_p(d_out),
+                                           ctypes.c_void_p(stream)), self._h)
 
     def forward(self, pixels) -> np.ndarray:
         """lib.rs:90-114. Returns float32 [batch, T, 384] (T = 201 at 224x224)."""

@@ -73,6 +73,27 @@ int dinov3_patch_mean(dinov3_model *m, const float *pixels, uint64_t n_floats, f
  * images; runs forward once, then dhx_benchmark. */
 int dinov3_benchmark(dinov3_model *m, const float *pixels, uint64_t n_floats, uint64_t samples,
                      dinov3_timings *out);
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). dinov3_forward on device memory, with every
+ * intermediate buffer (residual stream, q/k/v, attention and SwiGLU outputs,
+ * LayerNorm statistics, split-K slabs) in a fixed array of
+ * DINOV3_NOALLOC_SCRATCH_BYTES per GPU, which the library holds from the
+ * first model load on that GPU until the process ends, instead of the
+ * model's own buffers. pixels: images x 3 x S x S float32 NCHW, out:
+ * images x T x 384 float32, both device memory on the model's GPU, 16-byte
+ * aligned. The launches (the same kernels and plan as dinov3_forward, so the
+ * same results bit for bit) are queued on `stream` (a hipStream_t of that
+ * GPU; NULL = the model's own stream) and the call returns without waiting:
+ * synchronise the stream before reading `out`. It calls no hipMalloc,
+ * hipFree or other allocating routine, records no graph and does not check
+ * that the pixels are finite. A batch whose buffers do not fit the array (beyond about 43 images
+ * at 224x224, 9 at 512x512) fails with an error naming the sizes, before
+ * anything is queued. Every call on one GPU uses that GPU's single array and
+ * leaves its data there: calls that overlap in time on one GPU (other
+ * streams, threads or models) race and give wrong results. */
+#define DINOV3_NOALLOC_SCRATCH_BYTES (64ull << 20)
+int dinov3_forward_noalloc(dinov3_model *m, const float *pixels, uint64_t images, float *out, void *stream);
 const char *dinov3_last_error(const dinov3_model *m);
 void dinov3_free(dinov3_model *m);
 
