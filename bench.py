@@ -182,6 +182,11 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--batch", type=int, default=64)
+    ap.add_argument("--image-size", type=int, default=224,
+                    help="224: the headline (batch 64) with batch 32, batch 1, end-to-end and 512x512 legs beside it; "
+                         "512: BASELINE.json config 5 alone (use --batch 8), for profiling that workload")
+    ap.add_argument("--sync-samples", type=int, default=100,
+                    help="synchronised replays for the median / p95 (at least 10)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--branches", type=int, default=0,
@@ -199,19 +204,22 @@ def main():
 
     import dinov3_hrx as d
 
-    b = args.batch
+    b, S = args.batch, args.image_size
+    G = S // 16
+    T = G * G + 5
+    full = S == 224  # the headline run with its side legs
     with tempfile.TemporaryDirectory() as tmp:
         path = os.path.join(tmp, "weights.safetensors")
         d.write_random_weights(path, seed=0, preset=0)
-        model = d.DINOv3.load(path, d.Options(device=0, max_batch=max(b, 32)))
-        px = d.random_pixels(1, b)
+        model = d.DINOv3.load(path, d.Options(device=0, max_batch=max(b, 32) if full else b, image_size=S))
+        px = d.random_pixels(1, b, S)
 
         # Pick the down-projection variant (the reference uses the residual
         # GEMM for b > 1, split-K at b = 1) and the number of image groups run
         # side by side by a short trial; every choice gives the same bits.
         trial = {}
         for mode in (0, 1):
-            for nb in ([args.branches] if args.branches else [1, 2, 3, 4]):
+            for nb in ([args.branches] if args.branches else range(1, max(1, min(4, b // 4)) + 1)):
                 model.set_splitk(mode)
                 model.set_branches(nb)
                 model.stage(px)
@@ -226,70 +234,16 @@ def main():
             model.replay(b)
         sec = timed_replays(model, b, args.steps)
         value = b / sec
-        sync = sync_stats(model, b, max(100, args.steps))
+        sync = sync_stats(model, b, max(10, args.sync_samples))
 
-        # Batch 32 (config 2) on the same resident model, with its own short
-        # trial of the image grouping.
-        px32 = px[:32] if b >= 32 else d.random_pixels(1, 32)
-        trial32 = {}
-        for nb in ([args.branches] if args.branches else [1, 2, 3, 4]):
-            model.set_branches(nb)
-            model.stage(px32)
-            trial32[nb] = timed_replays(model, 32, 10)
-        branches32 = min(trial32, key=trial32.get)
-        model.set_branches(branches32)
-        model.stage(px32)
-        for _ in range(args.warmup):
-            model.replay(32)
-        sec32 = timed_replays(model, 32, args.steps)
-        sync32 = sync_stats(model, 32, max(100, args.steps))
-        model.set_branches(branches)
-
-        # Batch 1 (the reference's own benchmark case: graph-replay latency of
-        # one image, split-K down projection as in lib.rs:218-225).
-        model.stage(px[:1])
-        for _ in range(args.warmup):
-            model.replay(1)
-        sec1, p95_1 = replay_distribution(model, 1, max(100, args.steps))
-
-        # End to end through the host API (PCIe-inclusive; never `value`):
-        # forward() of 4 chunks of b images from host memory to host memory,
-        # with the pipelined uploads and readbacks.
-        big = np.concatenate([px] * 4)
-        model.forward(big)
-        e2e = []
-        for _ in range(3):
-            t0 = time.perf_counter()
-            model.forward(big)
-            e2e.append(time.perf_counter() - t0)
-        e2e_rate = len(big) / sorted(e2e)[1]
+        if full:
+            sec32, sync32, branches32, sec1, p95_1, e2e_rate = side_legs(d, model, px, b, branches, args)
 
         # Per-launch device time (HIP events on the model's stream), each
         # kernel alone over the whole batch: the single-group plan.
         model.set_branches(1)
         model.stage(px)
-        launches = model.launch_timings(b, iters=20)
-        kernels = {}
-        for i, (name, ms) in enumerate(launches):
-            name = {"patch_embed_stats": "patch_embed", "qkv_rope_ln": "qkv_rope", "resid_stats": "resid",
-                    "swiglu_ln": "swiglu", "splitk_reduce_stats": "splitk_reduce"}.get(name, name)
-            if name == "resid":
-                # the down projection (k = 1536) follows the SwiGLU GEMM; the o-projection (k = 384) follows attention
-                name = "resid_1536" if launches[i - 1][0].startswith("swiglu") else "resid_384"
-            k = kernels.setdefault(name, {"count": 0, "ms": 0.0})
-            k["count"] += 1
-            k["ms"] += ms
-        T, G = 201, 14
-        table = []
-        for name, k in kernels.items():
-            flops, nbytes = kernel_work(name, b, T, G)
-            avg = k["ms"] / k["count"]
-            tf = flops / (avg * 1e-3) / 1e12
-            gbs = nbytes / (avg * 1e-3) / 1e9
-            table.append({"kernel": name, "launches": k["count"], "avg_us": round(avg * 1e3, 2),
-                          "total_us": round(k["ms"] * 1e3, 1), "tflops": round(tf, 1), "gbs": round(gbs, 1),
-                          "mfma_frac": round(tf / PEAK_TFLOPS, 4), "hbm_frac": round(gbs / PEAK_GBS, 4)})
-        table.sort(key=lambda r: -r["total_us"])
+        table = kernel_table(model.launch_timings(b, iters=20), b, T, G)
         dom = table[0]
         flops, nbytes = kernel_work(dom["kernel"], b, T, G)
         ridge = PEAK_TFLOPS * 1e12 / (PEAK_GBS * 1e9)
@@ -299,55 +253,131 @@ def main():
         else:
             roof = {"kernel": dom["kernel"], "bound": "hbm", "achieved": dom["gbs"], "peak": PEAK_GBS,
                     "unit": "GB/s", "frac": round(dom["gbs"] / PEAK_GBS, 4)}
-        roof["traffic"] = measured_traffic(dom["kernel"]) if b == 64 else None
+        roof["traffic"] = measured_traffic(dom["kernel"]) if (b == 64 and full) else None
         roof["algorithmic_bytes"] = nbytes
         roof["avg_us"] = dom["avg_us"]
         model.close()
 
-        # Config 4 beside it: 512x512 (1029 tokens), batch 8, the same weights.
-        hr = d.DINOv3.load(path, d.Options(device=0, max_batch=8, image_size=512))
-        pxh = d.random_pixels(2, 8, 512)
-        trial_hr = {}
-        for nb in ([args.branches] if args.branches else [1, 2]):
-            hr.set_branches(nb)
+        if full:
+            # Config 5 beside it: 512x512 (1029 tokens), batch 8, the same weights.
+            hr = d.DINOv3.load(path, d.Options(device=0, max_batch=8, image_size=512))
+            pxh = d.random_pixels(2, 8, 512)
+            trial_hr = {}
+            for nb in ([args.branches] if args.branches else [1, 2]):
+                hr.set_branches(nb)
+                hr.stage(pxh)
+                trial_hr[nb] = timed_replays(hr, 8, 5)
+            branches_hr = min(trial_hr, key=trial_hr.get)
+            hr.set_branches(branches_hr)
             hr.stage(pxh)
-            trial_hr[nb] = timed_replays(hr, 8, 5)
-        branches_hr = min(trial_hr, key=trial_hr.get)
-        hr.set_branches(branches_hr)
-        hr.stage(pxh)
-        for _ in range(5):
-            hr.replay(8)
-        sec_hr = timed_replays(hr, 8, max(10, args.steps // 4))
-        hr.close()
+            for _ in range(5):
+                hr.replay(8)
+            sec_hr = timed_replays(hr, 8, max(10, args.steps // 4))
+            hr.close()
 
-        cpu = None if args.no_cpu else cpu_baseline(path, args.cpu_seconds)
+        cpu = None if (args.no_cpu or not full) else cpu_baseline(path, args.cpu_seconds)
 
     for row in table:
         print(json.dumps(row), file=sys.stderr)
+    gflop_image = GFLOP_PER_IMAGE if full else sum(kernel_work(k, 1, T, G)[0] * n for k, n in
+                                                   (("patch_embed", 1), ("qkv_rope", 12), ("attention", 12),
+                                                    ("resid_384", 12), ("swiglu", 12), ("resid_1536", 12))) / 1e9
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "images/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(sec * 1e3, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f16", "data": "synthetic",
-        "config": {"workload": f"DINOv3 ViT-S+/16 forward, 224x224, batch {b}, resident hipGraph replay "
-                               "(BASELINE.json config 3)", "batch": b, "image_size": 224, "tokens": T,
+        "config": {"workload": f"DINOv3 ViT-S+/16 forward, {S}x{S}, batch {b}, resident hipGraph replay "
+                               f"(BASELINE.json config {3 if full else 5})", "batch": b, "image_size": S, "tokens": T,
                    "down_proj": "splitk" if mode == 1 else "resid", "branches": branches,
                    "weights": "seeded random init (BASELINE)"},
-        "mfma_frac_forward": round(value * GFLOP_PER_IMAGE / 1e3 / PEAK_TFLOPS, 4),
+        "mfma_frac_forward": round(value * gflop_image / 1e3 / PEAK_TFLOPS, 4),
         "sync_replay": sync,
-        "batch32": {"value": round(32 / sec32, 1), "ms_per_step": round(sec32 * 1e3, 4), "branches": branches32,
-                    "sync_replay": sync32},
-        "batch1": {"value": round(1 / sec1, 1), "ms_per_step": round(sec1 * 1e3, 4), "p95_ms": round(p95_1 * 1e3, 4),
-                   "what": "median synchronised graph-replay latency of one image (the reference's b = 1 case)"},
-        "highres_512_b8": {"value": round(8 / sec_hr, 1), "unit": "images/s", "ms_per_step": round(sec_hr * 1e3, 4),
-                           "branches": branches_hr, "what": "BASELINE.json config 5: 512x512, 1029 tokens, batch 8"},
-        "end_to_end": {"value": round(e2e_rate, 1), "unit": "images/s",
-                       "what": f"forward() of {4 * b} images from host memory to host memory (PCIe and host copies "
-                               f"included, chunks of {b} pipelined); not the metric"},
-        "roofline": roof,
-        "cpu_baseline": cpu,
-        "kernels": table,
     }
+    if full:
+        line.update({
+            "batch32": {"value": round(32 / sec32, 1), "ms_per_step": round(sec32 * 1e3, 4), "branches": branches32,
+                        "sync_replay": sync32},
+            "batch1": {"value": round(1 / sec1, 1), "ms_per_step": round(sec1 * 1e3, 4),
+                       "p95_ms": round(p95_1 * 1e3, 4),
+                       "what": "median synchronised graph-replay latency of one image (the reference's b = 1 case)"},
+            "highres_512_b8": {"value": round(8 / sec_hr, 1), "unit": "images/s",
+                               "ms_per_step": round(sec_hr * 1e3, 4), "branches": branches_hr,
+                               "what": "BASELINE.json config 5: 512x512, 1029 tokens, batch 8"},
+            "end_to_end": {"value": round(e2e_rate, 1), "unit": "images/s",
+                           "what": f"forward() of {4 * b} images from host memory to host memory (PCIe and host "
+                                   f"copies included, chunks of {b} pipelined); not the metric"},
+        })
+    line.update({"roofline": roof, "cpu_baseline": cpu, "kernels": table})
     print(json.dumps(line))
+
+
+def kernel_table(launches, b, T, G):
+    """Per-kernel rows (launch count, average and total device time, achieved
+    TFLOP/s and GB/s at algorithmic work) from one plan's launch timings,
+    largest total first."""
+    kernels = {}
+    for i, (name, ms) in enumerate(launches):
+        name = {"patch_embed_stats": "patch_embed", "qkv_rope_ln": "qkv_rope", "resid_stats": "resid",
+                "swiglu_ln": "swiglu", "splitk_reduce_stats": "splitk_reduce"}.get(name, name)
+        if name == "resid":
+            # the down projection (k = 1536) follows the SwiGLU GEMM; the o-projection (k = 384) follows attention
+            name = "resid_1536" if launches[i - 1][0].startswith("swiglu") else "resid_384"
+        k = kernels.setdefault(name, {"count": 0, "ms": 0.0})
+        k["count"] += 1
+        k["ms"] += ms
+    table = []
+    for name, k in kernels.items():
+        flops, nbytes = kernel_work(name, b, T, G)
+        avg = k["ms"] / k["count"]
+        tf = flops / (avg * 1e-3) / 1e12
+        gbs = nbytes / (avg * 1e-3) / 1e9
+        table.append({"kernel": name, "launches": k["count"], "avg_us": round(avg * 1e3, 2),
+                      "total_us": round(k["ms"] * 1e3, 1), "tflops": round(tf, 1), "gbs": round(gbs, 1),
+                      "mfma_frac": round(tf / PEAK_TFLOPS, 4), "hbm_frac": round(gbs / PEAK_GBS, 4)})
+    table.sort(key=lambda r: -r["total_us"])
+    return table
+
+
+def side_legs(d, model, px, b, branches, args):
+    """The headline run's side measurements on the same resident model:
+    batch 32 (config 2), batch 1 (the reference's own case) and forward()
+    end to end through host memory."""
+    # Batch 32 (config 2) on the same resident model, with its own short
+    # trial of the image grouping.
+    px32 = px[:32] if b >= 32 else d.random_pixels(1, 32)
+    trial32 = {}
+    for nb in ([args.branches] if args.branches else [1, 2, 3, 4]):
+        model.set_branches(nb)
+        model.stage(px32)
+        trial32[nb] = timed_replays(model, 32, 10)
+    branches32 = min(trial32, key=trial32.get)
+    model.set_branches(branches32)
+    model.stage(px32)
+    for _ in range(args.warmup):
+        model.replay(32)
+    sec32 = timed_replays(model, 32, args.steps)
+    sync32 = sync_stats(model, 32, max(10, args.sync_samples))
+    model.set_branches(branches)
+
+    # Batch 1 (the reference's own benchmark case: graph-replay latency of
+    # one image, split-K down projection as in lib.rs:218-225).
+    model.stage(px[:1])
+    for _ in range(args.warmup):
+        model.replay(1)
+    sec1, p95_1 = replay_distribution(model, 1, max(10, args.sync_samples))
+
+    # End to end through the host API (PCIe-inclusive; never `value`):
+    # forward() of 4 chunks of b images from host memory to host memory,
+    # with the pipelined uploads and readbacks.
+    big = np.concatenate([px] * 4)
+    model.forward(big)
+    e2e = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        model.forward(big)
+        e2e.append(time.perf_counter() - t0)
+    e2e_rate = len(big) / sorted(e2e)[1]
+    return sec32, sync32, branches32, sec1, p95_1, e2e_rate
 
 
 if __name__ == "__main__":

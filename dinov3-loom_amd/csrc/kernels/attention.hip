@@ -56,6 +56,104 @@ __device__ __forceinline__ void vm_barrier() {
     asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
+// The running softmax state of one lane's query (lane l holds query l % 32
+// and half of each 32-key sub-block's scores; see the top of this file).
+struct QueryState {
+    half8_t qf[4];                      // Q^T fragments, pre-scaled by 1/8
+    float16_t o[2];                     // O^T accumulators: channels 32ct + 8(r/4) + 4hi + r%4
+    float m_run = -1e30f, l_run = 0.f;  // running max (lazy) and denominator
+};
+
+// Transpose-read position of this lane inside a 4-key x 32-channel patch of
+// a V block: lane j of each 16-lane group receives channel 16*(group%2) + j
+// of four consecutive keys.
+__device__ __forceinline__ int tr_row_of(int lane) { return (lane & 15) >> 2; }
+__device__ __forceinline__ int tr_col_of(int lane) { return 16 * ((lane >> 4) & 1) + 4 * (lane & 3); }
+
+// One sub-block of 32 keys (rows row0 .. row0+31 of the swizzled K and V
+// blocks in LDS, keys key0 .. key0+31 of the sequence of T):
+// S^T = K Q^T, masked past T, lazy running max, P = 2^(s log2e - m log2e),
+// O^T += V^T P^T with P in f16 and the denominator in f32.
+__device__ __forceinline__ void attend32(QueryState& st, const half_t* sK, const half_t* sV, int row0, int key0,
+                                         int T, int lane) {
+    const int l32 = lane & 31, hi = lane >> 5;
+    const float neg_inf = -__builtin_inff();
+    float16_t s = {};
+    const int kr = row0 + l32;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) s = mfma32x32x16(*(const half8_t*)(sK + swz(kr, kk * 16 + hi * 8)), st.qf[kk], s);
+    // s[r] is the score of key key0 + 8(r/4) + 4*hi + r%4 for query l32.
+    if (key0 + 32 > T) {  // the last, partial block of keys (uniform)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            if (key0 + 8 * (r >> 2) + 4 * hi + (r & 3) >= T) s[r] = neg_inf;
+    }
+    float mx = s[0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
+    mx = half_pair_max(mx);  // every sub-block holds a valid key of each pair
+    // Lazy rescaling: the running max moves only when a score exceeds it by
+    // more than kLazy, so weights stay below e^kLazy (well inside f16 for P)
+    // and most sub-blocks skip rescaling O entirely.
+    const bool grow = mx > st.m_run + kLazy;
+    if (__any(grow)) {  // uniform across the wave
+        const float m_new = grow ? mx : st.m_run;
+        const float alpha = fast_exp2((st.m_run - m_new) * kLog2e);
+        st.l_run *= alpha;
+        st.o[0] *= alpha;
+        st.o[1] *= alpha;
+        st.m_run = m_new;
+    }
+    const float mb = st.m_run * kLog2e;
+    float sum = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        s[r] = fast_exp2(fmaf(s[r], kLog2e, -mb));
+        sum += s[r];
+    }
+    sum = half_pair_sum(sum);
+    st.l_run += sum;
+    // P^T as the b operand: k-slice element j of this lane is key
+    // key0 + 16ks + (j < 4 ? 4hi + j : 8 + 4hi + j - 4); the V^T transpose
+    // reads below give channel ct*32 + l32 of the same keys.
+    half8_t pb[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pb[ks][e] = (half_t)s[8 * ks + e];
+    const int tr_row = tr_row_of(lane), tr_col = tr_col_of(lane);
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const int vr = row0 + ks * 16 + 4 * hi + tr_row;
+            const half4_t a0 = lds_read_tr16(sV + swz(vr, ct * 32 + tr_col));
+            const half4_t a1 = lds_read_tr16(sV + swz(vr + 8, ct * 32 + tr_col));
+            const half8_t va = __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7);
+            st.o[ct] = mfma32x32x16(va, pb[ks], st.o[ct]);
+        }
+}
+
+// Output of one lane's query: O / l in f16 into out (fragment order): each
+// 16-channel half of a 32-channel block becomes one 8-channel piece per lane
+// after frag_swap.
+__device__ __forceinline__ void store_query(const QueryState& st, half_t* out, int row, int head, int hi) {
+    const float inv = 1.0f / st.l_run;
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            const float16_t& a = st.o[ct];
+            const half4_t g0 = {(half_t)(a[8 * kk] * inv), (half_t)(a[8 * kk + 1] * inv),
+                                (half_t)(a[8 * kk + 2] * inv), (half_t)(a[8 * kk + 3] * inv)};
+            const half4_t g1 = {(half_t)(a[8 * kk + 4] * inv), (half_t)(a[8 * kk + 5] * inv),
+                                (half_t)(a[8 * kk + 6] * inv), (half_t)(a[8 * kk + 7] * inv)};
+            const half8_t piece = frag_swap(g0, g1);
+            const int c = head * kHeadDim + ct * 32 + kk * 16 + hi * 8;
+            *(half8_t*)(out + frag_piece(row, c, kHidden)) = piece;
+        }
+}
+
 // NKB > 0: the number of key blocks of KB = 32 keys, known at compile time
 // (the block loop is then unrolled, which keeps the compiler's wait counts
 // exact; used for 201 tokens, whose 24 KB of LDS also leave room for other
@@ -66,6 +164,13 @@ struct KeyBlock {
     static constexpr int BLK = KB * kHeadDim;      // halfs per K (or V) block
     static constexpr int LOADS = KB / 32;          // DMA loads of 8 rows per matrix and wave
 };
+
+// DMA offsets of this lane for moving 8 key rows (one 1 KB load): lane i
+// lands at LDS slot (row i/8, chunk slot i%8) of rows r0 .. r0+7 and fetches
+// the chunk the swizzle puts there (r0 % 8 == 0, so row % 16 = r0 % 16 + i/8).
+__device__ __forceinline__ int dma_lane_offset(int lane, int r0) {
+    return (lane >> 3) * 128 + (((lane & 7) ^ swz_slot(r0 % 16 + (lane >> 3))) << 4);
+}
 
 template <int NKB>
 __global__ __launch_bounds__(kThreads, 3) void attention_kernel(AttentionArgs p) {
@@ -87,22 +192,19 @@ __global__ __launch_bounds__(kThreads, 3) void attention_kernel(AttentionArgs p)
     const int nkb = NKB > 0 ? NKB : (T + KBT::KB - 1) / KBT::KB;  // nkb * KB <= tpad, so every block row exists
 
     // Block kb of K and V: each wave moves KB/4 key rows of each, as 1 KB
-    // DMA loads of 8 rows. Lane i lands at LDS slot (row i/8, chunk slot
-    // i%8) and fetches the chunk the swizzle puts there.
+    // DMA loads of 8 rows.
     const uint32_t bytes = (uint32_t)p.tpad * kHeadDim * 2;
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<half_t*>(p.k + bh * p.tpad * kHeadDim), 0, bytes, kBufferRsrcWord3);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<half_t*>(p.v + bh * p.tpad * kHeadDim), 0, bytes, kBufferRsrcWord3);
-    // Wave w moves key rows (KB/4) w .. +KB/4-1 as KB/32 loads of 8 rows
-    // per matrix; load j covers rows r0 = (KB/4) w + 8j, so row % 16 =
-    // r0 % 16 + lane / 8.
+    // Wave w moves key rows (KB/4) w .. +KB/4-1 as KB/32 loads of 8 rows per
+    // matrix; load j covers rows (KB/4) w + 8j.
     // Sized 2, not KBT::LOADS: with a local array whose size depends on the
     // template parameter this compiler silently drops the host launch stub.
     int voff[2];
 #pragma unroll
-    for (int j = 0; j < KBT::LOADS; ++j)
-        voff[j] = (lane >> 3) * 128 + (((lane & 7) ^ swz_slot(((tid >> 6) * (KBT::KB / 4) + 8 * j) % 16 + (lane >> 3))) << 4);
+    for (int j = 0; j < KBT::LOADS; ++j) voff[j] = dma_lane_offset(lane, (tid >> 6) * (KBT::KB / 4) + 8 * j);
     auto dma = [&](half_t* k_buf, half_t* v_buf, int kb) {
 #pragma unroll
         for (int j = 0; j < KBT::LOADS; ++j) {
@@ -122,9 +224,10 @@ __global__ __launch_bounds__(kThreads, 3) void attention_kernel(AttentionArgs p)
     // Queries past T load row T-1 (unconditional loads keep the wait counts
     // exact); their results are never stored.
     const int qrow = qb * QB + wave * 32 + l32;
-    half8_t qf[4];
+    QueryState st;
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) qf[kk] = *(const half8_t*)(qg + (size_t)min(qrow, T - 1) * kHeadDim + kk * 16 + hi * 8);
+    for (int kk = 0; kk < 4; ++kk)
+        st.qf[kk] = *(const half8_t*)(qg + (size_t)min(qrow, T - 1) * kHeadDim + kk * 16 + hi * 8);
     asm volatile("" ::: "memory");
     if (NKB == 0 || nkb > 1) {  // with a runtime count, block 1 repeats block 0 when there is one block
         dma(sK1, sV1, min(1, nkb - 1));
@@ -133,19 +236,12 @@ __global__ __launch_bounds__(kThreads, 3) void attention_kernel(AttentionArgs p)
         vm_barrier<0>();
     }
 
-    // Transpose-read position of this lane inside a 4-key x 32-channel patch
-    // of the V block: lane j of each 16-lane group then receives channel
-    // 16*(group%2) + j of four consecutive keys.
-    const int tr_row = (lane & 15) >> 2, tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-
     // Scores are s = (q / 8) . k: Q is scaled by 1/8 once (a power of two,
     // exact for normal f16 values), and the softmax weight of a score is
     // 2^(s*log2e - m*log2e), one FMA and one v_exp_f32.
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) qf[kk] *= (half_t)0.125f;
-    const float neg_inf = -__builtin_inff();
-    float16_t o[2] = {float16_t{}, float16_t{}};
-    float m_run = -1e30f, l_run = 0.f;
+    for (int kk = 0; kk < 4; ++kk) st.qf[kk] *= (half_t)0.125f;
+    st.o[0] = st.o[1] = float16_t{};
     // Waves whose 32 queries all lie past T only help move K and V.
     const bool active = qb * QB + wave * 32 < T;
 
@@ -154,60 +250,7 @@ __global__ __launch_bounds__(kThreads, 3) void attention_kernel(AttentionArgs p)
         for (int sub = 0; sub < KBT::KB / 32 && active; ++sub) {
             const int key0 = kb * KBT::KB + sub * 32;
             if (key0 >= T) break;  // uniform across the workgroup
-            float16_t s = {};
-            const int kr = sub * 32 + l32;
-#pragma unroll
-            for (int kk = 0; kk < 4; ++kk)
-                s = mfma32x32x16(*(const half8_t*)(sK + swz(kr, kk * 16 + hi * 8)), qf[kk], s);
-            // s[r] is the score of key key0 + 8(r/4) + 4*hi + r%4 for query l32.
-            if (key0 + 32 > T) {  // the last, partial block of keys (uniform)
-#pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    if (key0 + 8 * (r >> 2) + 4 * hi + (r & 3) >= T) s[r] = neg_inf;
-            }
-            float mx = s[0];
-#pragma unroll
-            for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
-            mx = half_pair_max(mx);  // every sub-block holds a valid key of each pair
-            // Lazy rescaling: the running max moves only when a score exceeds
-            // it by more than kLazy, so weights stay below e^kLazy (well inside
-            // f16 for P) and most sub-blocks skip rescaling O entirely.
-            const bool grow = mx > m_run + kLazy;
-            if (__any(grow)) {  // uniform across the wave
-                const float m_new = grow ? mx : m_run;
-                const float alpha = fast_exp2((m_run - m_new) * kLog2e);
-                l_run *= alpha;
-                o[0] *= alpha;
-                o[1] *= alpha;
-                m_run = m_new;
-            }
-            const float mb = m_run * kLog2e;
-            float sum = 0.f;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                s[r] = fast_exp2(fmaf(s[r], kLog2e, -mb));
-                sum += s[r];
-            }
-            sum = half_pair_sum(sum);
-            l_run += sum;
-            // P^T as the b operand: k-slice element j of this lane is key
-            // key0 + 16ks + (j < 4 ? 4hi + j : 8 + 4hi + j - 4); the V^T
-            // transpose reads below give channel ct*32 + l32 of the same keys.
-            half8_t pb[2];
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) pb[ks][e] = (half_t)s[8 * ks + e];
-#pragma unroll
-            for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-                for (int ks = 0; ks < 2; ++ks) {
-                    const int vr = sub * 32 + ks * 16 + 4 * hi + tr_row;
-                    const half4_t a0 = lds_read_tr16(sV + swz(vr, ct * 32 + tr_col));
-                    const half4_t a1 = lds_read_tr16(sV + swz(vr + 8, ct * 32 + tr_col));
-                    const half8_t va = __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7);
-                    o[ct] = mfma32x32x16(va, pb[ks], o[ct]);
-                }
+            attend32(st, sK, sV, sub * 32, key0, T, lane);
         }
     };
     // Block kb is computed from buffer kb % 3 while the DMA of block kb+2
@@ -248,25 +291,134 @@ __global__ __launch_bounds__(kThreads, 3) void attention_kernel(AttentionArgs p)
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
 
-    if (qrow < T) {
-        // out is in fragment order: each 16-channel half of a 32-channel
-        // block becomes one 8-channel piece per lane after frag_swap.
-        const float inv = 1.0f / l_run;
-        const int row = img * T + qrow;
+    if (qrow < T) store_query(st, p.out, img * T + qrow, head, hi);
+}
+
+// Long sequences (512x512: 1029 tokens): each workgroup of 8 waves holds 128
+// queries as 4 query waves x 2 key halves. Half h walks key blocks
+// h*NH .. h*NH+NH-1 (32 keys each, NH known at compile time so the walk is
+// unrolled and every wait exact), streamed by its own 4 waves through its own
+// three DMA buffers; both halves meet at the same barriers. At the end the
+// second half's (running max, denominator, O^T) go through LDS to the first
+// half, which merges them (rescaling both to the larger max) and writes the
+// output. Twice the waves of attention_kernel for the same workgroups, so
+// the softmax VALU work of one wave overlaps the MFMAs and loads of others.
+constexpr int kSplitThreads = 512;
+constexpr int kSplitBlk = 32 * kHeadDim;  // halfs per 32-key K (or V) block
+
+// One key half's walk: blocks first .. first+NH-1 (past the sequence's last
+// block the DMA repeats that block and the compute is skipped), through the
+// half's own three K and three V buffers. The buffers are separate LDS
+// variables chosen at compile time (the caller branches on the half), so the
+// compiler can tell the buffer being read from the ones being filled and
+// adds no waits of its own for the DMA in flight.
+template <int NH>
+__device__ __forceinline__ void split_walk(QueryState& st, half_t* const (&kbuf)[3], half_t* const (&vbuf)[3],
+                                           const __amdgpu_buffer_rsrc_t& rk, const __amdgpu_buffer_rsrc_t& rv,
+                                           const half_t* qg, int first, int nkb, int qrow, bool active, int T,
+                                           int hwave, int lane) {
+    const int hi = lane >> 5;
+    const int voff = dma_lane_offset(lane, 8 * hwave), last = min(first + NH, nkb) - 1;
+    auto dma = [&](int buf, int s) {
+        const int kb = min(first + s, last), row = 8 * hwave, soff = (kb * 32 + row) * 128;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(kbuf[buf] + row * kHeadDim),
+                                                 16, voff, soff, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)(vbuf[buf] + row * kHeadDim),
+                                                 16, voff, soff, 0, 0);
+    };
+    // As in attention_kernel: block 0, the Q fragments, block 1; the first
+    // wait counts only block 1's two DMA loads.
+    dma(0, 0);
 #pragma unroll
-        for (int ct = 0; ct < 2; ++ct)
+    for (int kk = 0; kk < 4; ++kk)
+        st.qf[kk] = *(const half8_t*)(qg + (size_t)min(qrow, T - 1) * kHeadDim + kk * 16 + hi * 8);
+    asm volatile("" ::: "memory");
+    dma(1, 1);
+    vm_barrier<2>();
 #pragma unroll
-            for (int kk = 0; kk < 2; ++kk) {
-                const float16_t& a = o[ct];
-                const half4_t g0 = {(half_t)(a[8 * kk] * inv), (half_t)(a[8 * kk + 1] * inv),
-                                    (half_t)(a[8 * kk + 2] * inv), (half_t)(a[8 * kk + 3] * inv)};
-                const half4_t g1 = {(half_t)(a[8 * kk + 4] * inv), (half_t)(a[8 * kk + 5] * inv),
-                                    (half_t)(a[8 * kk + 6] * inv), (half_t)(a[8 * kk + 7] * inv)};
-                const half8_t piece = frag_swap(g0, g1);
-                const int c = head * kHeadDim + ct * 32 + kk * 16 + hi * 8;
-                *(half8_t*)(p.out + frag_piece(row, c, kHidden)) = piece;
-            }
+    for (int kk = 0; kk < 4; ++kk) st.qf[kk] *= (half_t)0.125f;
+    st.o[0] = st.o[1] = float16_t{};
+    // Step s: block first+s from buffer s % 3 while block s+2's DMA fills
+    // buffer (s+2) % 3 (released by the previous barrier); the barrier
+    // leaves only that DMA in flight, so block s+1 has landed for every wave.
+#pragma unroll
+    for (int s = 0; s < NH; ++s) {
+        if (s + 2 < NH) dma((s + 2) % 3, s + 2);
+        const int kb = first + s;
+        if (active && kb < nkb) attend32(st, kbuf[s % 3], vbuf[s % 3], 0, kb * 32, T, lane);
+        if (s + 2 < NH)
+            vm_barrier<2>();
+        else
+            vm_barrier<0>();
     }
+}
+
+template <int NH>
+__global__ __launch_bounds__(kSplitThreads, 2) void attention_split_kernel(AttentionArgs p) {
+    // Per half three K and three V blocks of 4 KB (48 KB), as separate
+    // variables (the compiler tells distinct variables apart, not the rows of
+    // one array); reused at the end for the merge.
+    __shared__ __attribute__((aligned(16))) half_t k00[kSplitBlk], k01[kSplitBlk], k02[kSplitBlk];
+    __shared__ __attribute__((aligned(16))) half_t v00[kSplitBlk], v01[kSplitBlk], v02[kSplitBlk];
+    __shared__ __attribute__((aligned(16))) half_t k10[kSplitBlk], k11[kSplitBlk], k12[kSplitBlk];
+    __shared__ __attribute__((aligned(16))) half_t v10[kSplitBlk], v11[kSplitBlk], v12[kSplitBlk];
+    const int nqb = (p.tokens + QB - 1) / QB, total = nqb * kHeads * p.images;
+    const int per = (total + 7) >> 3, g = blockIdx.x, t = (g & 7) * per + (g >> 3);
+    if ((g >> 3) >= per || t >= total) return;  // uniform per workgroup
+    const int qb = t % nqb, head = (t / nqb) % kHeads, img = t / (nqb * kHeads);
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int qw = wave & 3, half = wave >> 2;  // query wave; key half (uniform per wave)
+    const int l32 = lane & 31, hi = lane >> 5;
+    const int T = p.tokens, nkb = (T + 31) / 32;  // nkb <= 2 * NH and nkb * 32 <= tpad (launcher checks)
+    const size_t bh = (size_t)img * kHeads + head;
+    const uint32_t bytes = (uint32_t)p.tpad * kHeadDim * 2;
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<half_t*>(p.k + bh * p.tpad * kHeadDim), 0, bytes, kBufferRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<half_t*>(p.v + bh * p.tpad * kHeadDim), 0, bytes, kBufferRsrcWord3);
+    const half_t* qg = p.q + bh * p.tpad * kHeadDim;
+    const int qrow = qb * QB + qw * 32 + l32;
+    const bool active = qb * QB + qw * 32 < T;  // waves whose queries all lie past T only move K and V
+    QueryState st;
+    if (half == 0) {
+        half_t* const kb[3] = {k00, k01, k02};
+        half_t* const vb[3] = {v00, v01, v02};
+        split_walk<NH>(st, kb, vb, rk, rv, qg, 0, nkb, qrow, active, T, qw, lane);
+    } else {
+        half_t* const kb[3] = {k10, k11, k12};
+        half_t* const vb[3] = {v10, v11, v12};
+        split_walk<NH>(st, kb, vb, rk, rv, qg, NH, nkb, qrow, active, T, qw, lane);
+    }
+    // Merge: the second half hands its 34 values per lane (max, denominator,
+    // O^T) to the first through LDS; both are rescaled to the larger max.
+    // Every wave passed the walk's last barrier, which waited for all of its
+    // DMA loads, so the buffers are free. Value f of query wave qw sits in
+    // buffer f / 4 at [(f % 4) * 4 + qw][lane] (f is a constant, so each
+    // access names its buffer).
+    half_t* const bufs[12] = {k00, k01, k02, v00, v01, v02, k10, k11, k12, v10, v11, v12};
+    auto slot = [&](int f) -> float* {
+        return reinterpret_cast<float*>(bufs[f / 4]) + ((f % 4) * 4 + qw) * 64 + lane;
+    };
+    if (half == 1) {
+        *slot(0) = st.m_run;
+        *slot(1) = st.l_run;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            *slot(2 + r) = st.o[0][r];
+            *slot(18 + r) = st.o[1][r];
+        }
+    }
+    __syncthreads();
+    if (half == 1 || qrow >= T) return;
+    const float m1 = *slot(0), m = fmaxf(st.m_run, m1);
+    const float a0 = fast_exp2((st.m_run - m) * kLog2e), a1 = fast_exp2((m1 - m) * kLog2e);
+    st.l_run = st.l_run * a0 + *slot(1) * a1;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        st.o[0][r] = st.o[0][r] * a0 + *slot(2 + r) * a1;
+        st.o[1][r] = st.o[1][r] * a0 + *slot(18 + r) * a1;
+    }
+    store_query(st, p.out, img * T + qrow, head, hi);
 }
 
 }  // namespace
@@ -274,14 +426,16 @@ __global__ __launch_bounds__(kThreads, 3) void attention_kernel(AttentionArgs p)
 hipError_t launch_attention(const AttentionArgs& a, hipStream_t s) {
     const int total = (a.tokens + QB - 1) / QB * kHeads * a.images;
     const dim3 grid((total + 7) & ~7), block(kThreads);
-    // 224x224 (201 tokens): seven blocks of 32 keys, unrolled; otherwise blocks
-    // of 64 with a run-time count.
-    switch ((a.tokens + 31) / 32) {
-        case 7:
-            hipLaunchKernelGGL(attention_kernel<7>, grid, block, 0, s, a);
-            break;
-        default:
-            hipLaunchKernelGGL(attention_kernel<0>, grid, block, 0, s, a);
+    // 224x224 (201 tokens): seven blocks of 32 keys, unrolled. 512x512 (1029
+    // tokens, 33 blocks of 32): the split-key kernel with 17 blocks per half.
+    // Otherwise blocks of 64 with a run-time count.
+    const int nkb32 = (a.tokens + 31) / 32;
+    if (nkb32 == 7) {
+        hipLaunchKernelGGL(attention_kernel<7>, grid, block, 0, s, a);
+    } else if ((nkb32 + 1) / 2 == 17 && nkb32 * 32 <= a.tpad) {
+        hipLaunchKernelGGL(attention_split_kernel<17>, grid, dim3(kSplitThreads), 0, s, a);
+    } else {
+        hipLaunchKernelGGL(attention_kernel<0>, grid, block, 0, s, a);
     }
     return hipGetLastError();
 }

@@ -159,14 +159,34 @@ __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void qkv_rope_kerne
     ActFrags<T> al[2];
     init_frags(al, p.h, M, kHidden);
     WeightDma<T> wd(p.w, 3 * kHidden, kHidden);
-    // The epilogue's own operands are loaded ahead of the K loop and wait in
-    // LDS: the tile's column constants and its rows' LayerNorm (mean, rstd).
+    // The epilogue's own operands are loaded ahead of the K loop: the tile's
+    // column constants and its rows' LayerNorm (mean, rstd), which wait in
+    // LDS, and each row's RoPE angles (cos, sin of channels 8g + 4hi .. +3,
+    // g = 0..3), which wait in registers. v tiles and prefix rows rotate by
+    // cos 1, sin 0.
     float4_t raw[T::FM][3];
+    float4_t rco[T::FM][4], rsi[T::FM][4];
     float cb = 0.f, cw = 0.f;
     gemm_tile_dma<T, 1, kHidden / T::BK>(
         al, wd, wb0, wb1, wb2, NT, NT * ((M + T::BM - 1) / T::BM), kHidden / T::BK,
         [&](int m0, int n0) {
             const Frag<T> f(m0, n0);
+            const int part = f.n_base / kHidden;
+#pragma unroll
+            for (int j = 0; j < T::FM; ++j) {
+                const int m = min(f.row(j), M - 1);
+                const int tok = m - m / Tok * Tok;
+                const size_t angle_row = (size_t)max(tok - kPrefix, 0) * kHeadDim;
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    rco[j][g] = float4_t{1.f, 1.f, 1.f, 1.f};
+                    rsi[j][g] = float4_t{};
+                    if (part < 2 && tok >= kPrefix) {
+                        rco[j][g] = ld4(p.cos + angle_row + g * 8 + f.hi * 4);
+                        rsi[j][g] = ld4(p.sin + angle_row + g * 8 + f.hi * 4);
+                    }
+                }
+            }
             if constexpr (LN) {
 #pragma unroll
                 for (int j = 0; j < T::FM; ++j) {
@@ -204,26 +224,8 @@ __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void qkv_rope_kerne
             const int mr = f.row(j);
             const int m = min(mr, M - 1);  // rows past M are computed but never written out
             const int img = m / Tok, tok = m - img * Tok;
-            // RoPE angles of this row, gathered together before any use (lanes
-            // hold different rows); prefix rows and v rotate by cos 1, sin 0.
-            const size_t angle_row = (size_t)max(tok - kPrefix, 0) * kHeadDim;
-            float4_t co[4], si[4];
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                co[g] = float4_t{1.f, 1.f, 1.f, 1.f};
-                si[g] = float4_t{};
-                if (part < 2) {  // uniform per wave
-                    co[g] = ld4(p.cos + angle_row + g * 8 + f.hi * 4);
-                    si[g] = ld4(p.sin + angle_row + g * 8 + f.hi * 4);
-                }
-            }
-            if (tok < kPrefix) {
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    co[g] = float4_t{1.f, 1.f, 1.f, 1.f};
-                    si[g] = float4_t{};
-                }
-            }
+            const float4_t* const co = rco[j];
+            const float4_t* const si = rsi[j];
             RowNorm rn{0.f, 1.f};
             if constexpr (LN) {
                 const float2_t v = rows_norm[f.m_base - m0 + j * 32 + f.l32];
