@@ -82,6 +82,20 @@ __device__ __forceinline__ void attend32(QueryState& st, const half_t* sK, const
     const int kr = row0 + l32;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) s = mfma32x32x16(*(const half8_t*)(sK + swz(kr, kk * 16 + hi * 8)), st.qf[kk], s);
+    // The V^T operands do not depend on the softmax: read them now so their
+    // LDS latency hides under the exponentials. va[ct][ks] holds channel
+    // ct*32 + l32 of keys key0 + 16ks + (j < 4 ? 4hi + j : 8 + 4hi + j - 4).
+    const int tr_row = tr_row_of(lane), tr_col = tr_col_of(lane);
+    half8_t va[2][2];
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const int vr = row0 + ks * 16 + 4 * hi + tr_row;
+            const half4_t a0 = lds_read_tr16(sV + swz(vr, ct * 32 + tr_col));
+            const half4_t a1 = lds_read_tr16(sV + swz(vr + 8, ct * 32 + tr_col));
+            va[ct][ks] = __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7);
+        }
     // s[r] is the score of key key0 + 8(r/4) + 4*hi + r%4 for query l32.
     if (key0 + 32 > T) {  // the last, partial block of keys (uniform)
 #pragma unroll
@@ -114,24 +128,16 @@ __device__ __forceinline__ void attend32(QueryState& st, const half_t* sK, const
     sum = half_pair_sum(sum);
     st.l_run += sum;
     // P^T as the b operand: k-slice element j of this lane is key
-    // key0 + 16ks + (j < 4 ? 4hi + j : 8 + 4hi + j - 4); the V^T transpose
-    // reads below give channel ct*32 + l32 of the same keys.
+    // key0 + 16ks + (j < 4 ? 4hi + j : 8 + 4hi + j - 4), as in va.
     half8_t pb[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
         for (int e = 0; e < 8; ++e) pb[ks][e] = (half_t)s[8 * ks + e];
-    const int tr_row = tr_row_of(lane), tr_col = tr_col_of(lane);
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const int vr = row0 + ks * 16 + 4 * hi + tr_row;
-            const half4_t a0 = lds_read_tr16(sV + swz(vr, ct * 32 + tr_col));
-            const half4_t a1 = lds_read_tr16(sV + swz(vr + 8, ct * 32 + tr_col));
-            const half8_t va = __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7);
-            st.o[ct] = mfma32x32x16(va, pb[ks], st.o[ct]);
-        }
+        for (int ks = 0; ks < 2; ++ks) st.o[ct] = mfma32x32x16(va[ct][ks], pb[ks], st.o[ct]);
 }
 
 // Output of one lane's query: O / l in f16 into out (fragment order): each
