@@ -189,6 +189,8 @@ def main():
                     help="synchronised replays for the median / p95 (at least 10)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-legs", action="store_true",
+                    help="skip the batch-32, batch-1, end-to-end and 512x512 measurements (for profiling runs)")
     ap.add_argument("--branches", type=int, default=0,
                     help="image groups run as concurrent graph branches (0: pick 1-4 by a short trial)")
     ap.add_argument("--library-gemms", action="store_true",
@@ -207,7 +209,7 @@ def main():
     b, S = args.batch, args.image_size
     G = S // 16
     T = G * G + 5
-    full = S == 224  # the headline run with its side legs
+    full = S == 224 and not args.no_legs  # the headline run with its side legs
     with tempfile.TemporaryDirectory() as tmp:
         path = os.path.join(tmp, "weights.safetensors")
         d.write_random_weights(path, seed=0, preset=0)
@@ -253,7 +255,7 @@ def main():
         else:
             roof = {"kernel": dom["kernel"], "bound": "hbm", "achieved": dom["gbs"], "peak": PEAK_GBS,
                     "unit": "GB/s", "frac": round(dom["gbs"] / PEAK_GBS, 4)}
-        roof["traffic"] = measured_traffic(dom["kernel"]) if (b == 64 and full) else None
+        roof["traffic"] = measured_traffic(dom["kernel"]) if (b == 64 and S == 224) else None
         roof["algorithmic_bytes"] = nbytes
         roof["avg_us"] = dom["avg_us"]
         model.close()
@@ -279,7 +281,7 @@ def main():
 
     for row in table:
         print(json.dumps(row), file=sys.stderr)
-    gflop_image = GFLOP_PER_IMAGE if full else sum(kernel_work(k, 1, T, G)[0] * n for k, n in
+    gflop_image = GFLOP_PER_IMAGE if S == 224 else sum(kernel_work(k, 1, T, G)[0] * n for k, n in
                                                    (("patch_embed", 1), ("qkv_rope", 12), ("attention", 12),
                                                     ("resid_384", 12), ("swiglu", 12), ("resid_1536", 12))) / 1e9
     line = {
@@ -287,7 +289,7 @@ def main():
         "warmup": args.warmup, "ms_per_step": round(sec * 1e3, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f16", "data": "synthetic",
         "config": {"workload": f"DINOv3 ViT-S+/16 forward, {S}x{S}, batch {b}, resident hipGraph replay "
-                               f"(BASELINE.json config {3 if full else 5})", "batch": b, "image_size": S, "tokens": T,
+                               f"(BASELINE.json config {3 if S == 224 else 5})", "batch": b, "image_size": S, "tokens": T,
                    "down_proj": "splitk" if mode == 1 else "resid", "branches": branches,
                    "weights": "seeded random init (BASELINE)"},
         "mfma_frac_forward": round(value * gflop_image / 1e3 / PEAK_TFLOPS, 4),
