@@ -17,8 +17,10 @@ import json
 import os
 import re
 import statistics
+import subprocess
 import sys
 import tempfile
+import threading
 import time
 
 import numpy as np
@@ -101,6 +103,70 @@ def sync_stats(model, b, samples):
     med, p95 = replay_distribution(model, b, samples)
     return {"median_ms": round(med * 1e3, 4), "p95_ms": round(p95 * 1e3, 4), "samples": samples,
             "images_per_s_at_median": round(b / med, 1)}
+
+
+def read_sclk_mhz():
+    """Current shader clock from rocm-smi (None where it is unavailable)."""
+    try:
+        out = subprocess.run(["rocm-smi", "--showclocks"], capture_output=True, text=True, timeout=20).stdout
+    except (OSError, subprocess.SubprocessError):
+        return None
+    m = re.search(r"sclk clock level: \d+: \((\d+)Mhz\)", out)
+    return int(m.group(1)) if m else None
+
+
+def sustained(model, b, seconds=4.0, chunk=40):
+    """Throughput over several seconds of back-to-back replays (synchronised
+    every `chunk` replays) with the shader clock sampled meanwhile: the GPU
+    lowers its clock under sustained MFMA load, so this rate sits below the
+    short timed region's."""
+    clocks, stop = [], threading.Event()
+
+    def sampler():
+        while not stop.is_set():
+            v = read_sclk_mhz()
+            if v is None:
+                return
+            clocks.append(v)
+            stop.wait(0.1)
+
+    th = threading.Thread(target=sampler, daemon=True)
+    th.start()
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(chunk):
+            model.replay(b)
+        model.synchronize()
+        n += chunk
+    dt = time.perf_counter() - t0
+    stop.set()
+    th.join()
+    settled = clocks[len(clocks) // 4:] or clocks
+    return {"value": round(n * b / dt, 1), "seconds": round(dt, 2),
+            "sclk_mhz": ({"median": int(statistics.median(settled)), "min": min(settled), "max": max(settled),
+                          "samples": len(clocks)} if clocks else None),
+            "what": "back-to-back replays for several seconds, shader clock from rocm-smi (first quarter of the "
+                    "samples dropped while it settles)"}
+
+
+def ceilings(d, full=False):
+    """Machine ceilings from dhx_probe (one wave per SIMD, 32x32x16 f16 MFMAs):
+    the MFMA loop alone on random and on zero operands, and with full=True the
+    vector work and the load rates that still leave the MFMAs unslowed."""
+    out = {"mfma_random": d.probe("mfma_random"), "mfma_zeros": d.probe("mfma_zeros")}
+    if full:
+        out["valu_fma_per_mfma"] = {n: d.probe("valu", n) for n in (0, 2, 4, 6, 8)}
+        out["exp2_per_mfma"] = {n: d.probe("exp2", n) for n in (1, 2)}
+        for where in ("l1", "l2", "hbm"):
+            rows = {n: d.probe(f"loads_{where}", n) for n in (0, 2, 3, 4, 6)}
+            for n, r in rows.items():  # per-CU load rate: 4 waves x n KB per 8-MFMA iteration
+                r["cu_bytes_per_clk"] = round(4 * n * 1024 / r["cycles_per_8_mfma"], 1)
+            out[f"loads_{where}_per_8_mfma"] = rows
+    for v in out.values():
+        for r in (v.values() if "tflops" not in v else [v]):
+            for k in ("cycles_per_8_mfma", "tflops", "clock_ghz"):
+                r[k] = round(r[k], 3 if k == "clock_ghz" else 1)
+    return out
 
 
 def cpu_model():
@@ -195,9 +261,16 @@ def main():
                     help="image groups run as concurrent graph branches (0: pick 1-4 by a short trial)")
     ap.add_argument("--library-gemms", action="store_true",
                     help="only time the vendor library's GEMMs at the forward's shapes (a reference table)")
+    ap.add_argument("--ceilings", action="store_true",
+                    help="only run the machine-ceiling probes (MFMA issue, power-limited clock, co-issued vector "
+                         "work, load rates) and print them as one JSON line")
     args = ap.parse_args()
     if args.library_gemms:
         library_gemms(args.batch)
+        return
+    if args.ceilings:
+        import dinov3_hrx as d
+        print(json.dumps(ceilings(d, full=True)))
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the forward would shard by image, "
@@ -237,6 +310,7 @@ def main():
         sec = timed_replays(model, b, args.steps)
         value = b / sec
         sync = sync_stats(model, b, max(10, args.sync_samples))
+        steady = sustained(model, b) if full else None
 
         if full:
             sec32, sync32, branches32, sec1, p95_1, e2e_rate = side_legs(d, model, px, b, branches, args)
@@ -256,6 +330,15 @@ def main():
             roof = {"kernel": dom["kernel"], "bound": "hbm", "achieved": dom["gbs"], "peak": PEAK_GBS,
                     "unit": "GB/s", "frac": round(dom["gbs"] / PEAK_GBS, 4)}
         roof["traffic"] = measured_traffic(dom["kernel"]) if (b == 64 and S == 224) else None
+        ceiling = ceilings(d) if full else None
+        if ceiling:
+            # The MFMA loop alone on random operands, on this GPU and its power
+            # budget: what the published peak shrinks to once the clock drops.
+            ceil_random = ceiling["mfma_random"]
+            if roof["bound"] == "mfma":
+                roof["attainable"] = {"peak": ceil_random["tflops"], "clock_ghz": ceil_random["clock_ghz"],
+                                      "frac": round(dom["tflops"] / ceil_random["tflops"], 4),
+                                      "what": "MFMA-only loop on random f16 operands, one wave per SIMD (dhx_probe)"}
         roof["algorithmic_bytes"] = nbytes
         roof["avg_us"] = dom["avg_us"]
         model.close()
@@ -305,11 +388,12 @@ def main():
             "highres_512_b8": {"value": round(8 / sec_hr, 1), "unit": "images/s",
                                "ms_per_step": round(sec_hr * 1e3, 4), "branches": branches_hr,
                                "what": "BASELINE.json config 5: 512x512, 1029 tokens, batch 8"},
+            "sustained": steady,
             "end_to_end": {"value": round(e2e_rate, 1), "unit": "images/s",
                            "what": f"forward() of {4 * b} images from host memory to host memory (PCIe and host "
                                    f"copies included, chunks of {b} pipelined); not the metric"},
         })
-    line.update({"roofline": roof, "cpu_baseline": cpu, "kernels": table})
+    line.update({"roofline": roof, "cpu_baseline": cpu, "ceilings": ceiling, "kernels": table})
     print(json.dumps(line))
 
 

@@ -24,6 +24,7 @@ SOURCES = [
     "kernels/gemm.hip",
     "kernels/attention.hip",
     "kernels/norm.hip",
+    "kernels/probe.hip",
     "engine.cpp",
     "model.cpp",
     "weights.cpp",

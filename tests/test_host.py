@@ -52,6 +52,13 @@ def test_binding_structs_match_header(tmp_path):
                      ctypes.sizeof(d._Options), ctypes.sizeof(d._Timings)]
 
 
+def test_probe_rejects_unsupported_arguments():
+    # Checked before any HIP call, so this runs without a GPU.
+    for kind, param in (("valu", 3), ("exp2", 0), ("loads_l2", 5), ("mfma_random", 1)):
+        with pytest.raises(d.DINOv3Error, match="unsupported probe"):
+            d.probe(kind, param)
+
+
 def test_constants_match_reference():
     assert d.IMAGE_ELEMENTS == 3 * 224 * 224 and d.TOKENS == 201 and d.HIDDEN == 384
 

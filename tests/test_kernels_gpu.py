@@ -724,3 +724,15 @@ def test_mfma_accumulation_mixed_magnitudes(eng, case):
     # or without outliers, i.e. products are not truncated to the largest
     # one's exponent; the bar leaves 8x margin.
     assert worst_max < 2.0**-14 and worst_sum < 2.0**-18
+
+
+def test_machine_ceiling_probes():
+    # One wave per SIMD issues independent 32x32x16 f16 MFMAs every 32 cycles
+    # (8 per 256), and 2 L1-resident 16-byte loads per 8 MFMAs leave that
+    # rate intact; the implied clock is a plausible shader clock.
+    r = d.probe("mfma_random")
+    assert 250 <= r["cycles_per_8_mfma"] <= 270, r
+    assert 0.5 <= r["clock_ghz"] <= 2.6, r
+    assert r["tflops"] > 0.5 * 2500 * r["clock_ghz"] / 2.4, r
+    l1 = d.probe("loads_l1", 2)
+    assert l1["cycles_per_8_mfma"] <= 1.1 * r["cycles_per_8_mfma"], l1
