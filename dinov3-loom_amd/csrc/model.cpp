@@ -261,8 +261,11 @@ public:
     // its own slice of every buffer: the kernels of one group fill the last,
     // partial wave of workgroups of the other's. A row's arithmetic does not
     // depend on the group it is in, so results are bitwise the same. The down
-    // projection uses split-K slabs + reduce at batch 1 (as the reference) or
-    // when selected, else the residual GEMM. By default LayerNorm is folded
+    // projection is the residual GEMM, or split-K slabs + reduce when selected
+    // (the reference takes split-K at batch 1, lib.rs:218-225; here the
+    // residual GEMM is faster at batch 1 too, one launch instead of two per
+    // block, and keeps every image's result independent of the batch size).
+    // By default LayerNorm is folded
     // into the QKV and gate/up GEMMs, fed by row statistics that the
     // producers of x write (62 launches per group at b > 1); the unfused plan
     // runs LayerNorm kernels as the reference does (86).
@@ -318,7 +321,7 @@ public:
         const dhx_region A = frag_part(kAttn, kHiddenU), F = frag_part(kAct, 1536);
         const dhx_region O = part(out_buffer(slot), row * 4), I = part(image_buffer(slot), image_elems_ * 4);
         const dhx_region SL = part(kPartials, (uint64_t)kSplits * row * 4);  // [splits][rows][384] per group
-        const bool split = b == 1 || splitk_ == 1;
+        const bool split = splitk_ == 1;
         if (fused_ln_) {
             add(DHX_K_PATCH_EMBED_STATS, {B, G}, {I, w("patch_w"), w("patch_b"), w("prefix"), w("prefix_stats"), X, S});
         } else {
@@ -381,7 +384,7 @@ public:
         if (images > 64) throw Error("the allocation-free forward takes at most 64 images per call");
         const uint64_t r = images * tokens_, rf = (r + 31) / 32 * 32;
         const uint64_t heads = images * 6 * tpad_ * 64 * 2;
-        const bool split = images == 1 || splitk_ == 1;
+        const bool split = splitk_ == 1;
         uint64_t need[kBuffers] = {};
         need[kX] = rf * kHiddenU * 2;
         need[kH] = fused_ln_ ? 0 : rf * kHiddenU * 2;
@@ -425,7 +428,7 @@ public:
 
     // Graph key: batch size plus one bit per plan variant.
     uint64_t key(uint64_t b, uint32_t slot = 0) const {
-        return b | (splitk_ && b > 1 ? (1ull << 32) : 0) | (fused_ln_ ? 0 : (1ull << 33)) |
+        return b | (splitk_ ? (1ull << 32) : 0) | (fused_ln_ ? 0 : (1ull << 33)) |
                ((uint64_t)(groups(b) - 1) << 34) | ((uint64_t)slot << 36);
     }
 

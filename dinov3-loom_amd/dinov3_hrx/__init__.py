@@ -278,7 +278,7 @@ class DINOv3:
         _check_engine(_lib.dhx_synchronize(e), e)
 
     def set_splitk(self, mode: int) -> None:
-        """0: residual GEMM for the down projection at batch > 1; 1: split-K + reduce."""
+        """Down projection: 0 (default) the residual GEMM, 1 split-K + reduce, at every batch size."""
         _check(_lib.dinov3_set_splitk(self._h, int(mode)), self._h)
 
     def set_layernorm_fusion(self, on: bool) -> None:

@@ -107,10 +107,12 @@ dhx_engine *dinov3_engine(dinov3_model *m);
  * counterpart (the GPU half of forward, for timing). */
 int dinov3_stage(dinov3_model *m, const float *pixels, uint64_t n_floats);
 int dinov3_replay(dinov3_model *m, uint64_t images);
-/* Select the down-projection variant for batches > 1: 0 = residual GEMM
- * (the reference's choice for b > 1, lib.rs:226-232), 1 = split-K slabs +
- * reduce (lib.rs:218-225; the reference's b = 1 path). Batch 1 always uses
- * split-K as in the reference. Graphs already recorded are dropped. */
+/* Select the down-projection variant: 0 (default) = residual GEMM at every
+ * batch size (the reference's choice for b > 1, lib.rs:226-232; at b = 1 the
+ * reference takes split-K, lib.rs:218-225, but here the residual GEMM is
+ * faster there too and gives each image the same bits at every batch size),
+ * 1 = split-K slabs + reduce at every batch size. Graphs are kept per
+ * (batch, variant). */
 int dinov3_set_splitk(dinov3_model *m, int mode);
 /* LayerNorm plan (no reference counterpart): 1 (default) folds LayerNorm
  * into the QKV and gate/up GEMMs from row statistics written by the kernels

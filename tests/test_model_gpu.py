@@ -171,9 +171,9 @@ def test_batch_64_stress_every_grouping(models, oracle_weights):
 def test_512_batch_8_grouped_plan(models, oracle_weights):
     # Config 5 as bench.py runs it: 512x512 (1029 tokens), b = 8 in two
     # concurrent image groups of 4. One image per group against the oracle;
-    # the batch bitwise equal to one group and to batches of 2 (a batch of 1
-    # takes the split-K down projection, lib.rs:218-225, so it is not
-    # bitwise the same).
+    # the batch bitwise equal to one group, to batches of 2 and, for those
+    # two images, to batches of 1 (the default plan uses the residual GEMM
+    # at every batch size, so an image's bits do not depend on the batch).
     m = models(1, max_batch=8, image_size=512)
     px = d.random_pixels(23, 8, 512)
     out = m.forward(px)
@@ -188,6 +188,8 @@ def test_512_batch_8_grouped_plan(models, oracle_weights):
         m.set_branches(3)
     assert np.array_equal(m.forward(px[:2]), out[:2])
     assert np.array_equal(m.forward(px[6:]), out[6:])
+    assert np.array_equal(m.forward(px[:1]), out[:1])
+    assert np.array_equal(m.forward(px[7:]), out[7:])
 
 
 @pytest.mark.parametrize("dtype", ["F16", "BF16"])
@@ -260,17 +262,23 @@ def test_branches_are_bitwise_identical(models):
 
 
 def test_splitk_variant(models):
+    # Both down-projection variants at batch 8 and at batch 1 (the
+    # reference's split-K case, lib.rs:218-225): the same result to f16
+    # rounding; switching back restores the residual plan's bits.
     m = models(1, max_batch=8)
     px = d.random_pixels(5, 8)
     base = m.forward(px)
     m.set_splitk(1)
     try:
         split = m.forward(px)
+        split1 = m.forward(px[:1])
     finally:
         m.set_splitk(0)
     for i in range(8):
         assert cosine(split[i], base[i]) > 0.99999
+    assert np.array_equal(split1, split[:1])
     assert np.array_equal(m.forward(px), base)
+    assert np.array_equal(m.forward(px[:1]), base[:1])
 
 
 @pytest.mark.parametrize("preset", [0, 1])

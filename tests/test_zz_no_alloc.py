@@ -1,7 +1,8 @@
 """dinov3_forward_noalloc (include/dinov3.h) through the C ABI, against
 dinov3_forward on the same images: bitwise the same outputs on two calls in a
 row, the second smaller than the first, on a stream of the caller's and on
-the model's own stream; batch 1 (split-K plan) and 512x512; a batch beyond the
+the model's own stream; batch 1 with the split-K plan (its f32 slabs in the
+array too) and 512x512; a batch beyond the
 scratch array refused before anything is queued. Device memory for the
 inputs and outputs comes from the HIP runtime the library itself links
 (/opt/rocm), allocated here by the test, never by the entry point."""
@@ -82,12 +83,16 @@ def test_noalloc_matches_forward(hip, weight_file):
                 want = m.forward(px)
                 print(f"noalloc {images} images: max |diff| {np.abs(got - want).max()}")
                 assert np.array_equal(got, want), images
-            # batch 1 (split-K down projection) on the model's own stream
+            # batch 1 with the split-K down projection, on the model's own stream
             px = d.random_pixels(43, 1)
             dpx, dout = dev.upload(px), dev.alloc(201 * 384 * 4)
-            m.forward_noalloc(dpx, 1, dout, 0)
-            m.synchronize()
-            assert np.array_equal(dev.download(dout, (1, 201, 384)), m.forward(px))
+            m.set_splitk(1)
+            try:
+                m.forward_noalloc(dpx, 1, dout, 0)
+                m.synchronize()
+                assert np.array_equal(dev.download(dout, (1, 201, 384)), m.forward(px))
+            finally:
+                m.set_splitk(0)
             # a batch the array cannot hold is refused before anything is queued
             big = dev.alloc(44 * 3 * 224 * 224 * 4)
             with pytest.raises(d.DINOv3Error, match="bytes of scratch"):
