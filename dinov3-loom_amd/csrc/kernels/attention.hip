@@ -20,7 +20,8 @@
 // cross-half exchange, and the running rescale of O^T is a per-lane scalar.
 // Q is scaled by 1/8 in registers and log2(e) is folded into one FMA per
 // score, so the softmax runs on v_exp_f32; the running max is updated lazily
-// (only when it grows by more than kLazy), which skips most rescales of O.
+// (only when a block's weights against it sum past e^kLazy), which skips
+// most rescales of O and, on the common path, the block max itself.
 // P is rounded to f16 for the PV product; the denominator keeps the fp32
 // weights (as in the reference, attention_online_f16_wmma_cf16.loom:195-216).
 #include "launch.hpp"
@@ -31,6 +32,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int QB = 128;                  // queries per workgroup
 constexpr float kLazy = 8.0f;            // running-max slack of the lazy rescaling (score units)
+constexpr float kLazySum = 2980.957987f; // e^kLazy: the largest weight sum that needs no rescale
 
 // LDS on gfx950 has 64 banks of 4 bytes: two 128-byte key rows per bank
 // cycle. Chunk c of key row r sits at slot c ^ swz_slot(r), with
@@ -102,30 +104,42 @@ __device__ __forceinline__ void attend32(QueryState& st, const half_t* sK, const
         for (int r = 0; r < 16; ++r)
             if (key0 + 8 * (r >> 2) + 4 * hi + (r & 3) >= T) s[r] = neg_inf;
     }
-    float mx = s[0];
+    // Weights against the running max; the block max is needed only when
+    // some lane's weights sum past e^kLazy (a weight may then exceed it):
+    // the first block of a walk (m_run starts at -1e30, so the sum is inf)
+    // and blocks whose scores grew by more than kLazy. Those lanes move
+    // their max to the block's, rescale O and l, and recompute; every
+    // weight is then at most its sum, at most e^kLazy, well inside f16.
+    float p[16];
+    float mb = st.m_run * kLog2e;
+    float sum = 0.f;
 #pragma unroll
-    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
-    mx = half_pair_max(mx);  // every sub-block holds a valid key of each pair
-    // Lazy rescaling: the running max moves only when a score exceeds it by
-    // more than kLazy, so weights stay below e^kLazy (well inside f16 for P)
-    // and most sub-blocks skip rescaling O entirely.
-    const bool grow = mx > st.m_run + kLazy;
+    for (int r = 0; r < 16; ++r) {
+        p[r] = fast_exp2(fmaf(s[r], kLog2e, -mb));
+        sum += p[r];
+    }
+    sum = half_pair_sum(sum);
+    const bool grow = !(sum <= kLazySum);  // also true for inf (first block)
     if (__any(grow)) {  // uniform across the wave
-        const float m_new = grow ? mx : st.m_run;
+        float mx = s[0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
+        mx = half_pair_max(mx);  // every sub-block holds a valid key of each pair
+        const float m_new = grow ? fmaxf(mx, st.m_run) : st.m_run;
         const float alpha = fast_exp2((st.m_run - m_new) * kLog2e);
         st.l_run *= alpha;
         st.o[0] *= alpha;
         st.o[1] *= alpha;
         st.m_run = m_new;
-    }
-    const float mb = st.m_run * kLog2e;
-    float sum = 0.f;
+        mb = m_new * kLog2e;
+        sum = 0.f;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        s[r] = fast_exp2(fmaf(s[r], kLog2e, -mb));
-        sum += s[r];
+        for (int r = 0; r < 16; ++r) {
+            p[r] = fast_exp2(fmaf(s[r], kLog2e, -mb));
+            sum += p[r];
+        }
+        sum = half_pair_sum(sum);
     }
-    sum = half_pair_sum(sum);
     st.l_run += sum;
     // P^T as the b operand: k-slice element j of this lane is key
     // key0 + 16ks + (j < 4 ? 4hi + j : 8 + 4hi + j - 4), as in va.
@@ -133,7 +147,7 @@ __device__ __forceinline__ void attend32(QueryState& st, const half_t* sK, const
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) pb[ks][e] = (half_t)s[8 * ks + e];
+        for (int e = 0; e < 8; ++e) pb[ks][e] = (half_t)p[8 * ks + e];
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct)
 #pragma unroll

@@ -268,6 +268,35 @@ def test_attention(eng, images, grid, qscale):
         check(y[sl], ref, atol=2.0**-9 * np.abs(v[sl]).max(), cos_min=0.9999, what=f"attention T={T} img {i}")
 
 
+@pytest.mark.parametrize("case", ["ramp", "spike"])
+@pytest.mark.parametrize("grid", [14, 32])
+def test_attention_running_max_moves(eng, case, grid):
+    """Scores that keep growing along the keys (ramp: key norms rise 4x
+    from the first key to the last, so the running max moves in many blocks
+    and for some lanes of a wave but not others) or jump once in the last,
+    partial block (spike: one key aligned with every query, ~20 score units
+    above the rest): the rescaling path against the f64 oracle."""
+    rng = np.random.default_rng(grid * 7 + (case == "spike"))
+    T = grid * grid + 5
+    tpad = (T + 127) // 128 * 128
+    if case == "ramp":
+        q = f16(rng.normal(size=(T, 384)) * 2.0)
+        k = f16(rng.normal(size=(T, 384)) * np.linspace(1.0, 4.0, T)[:, None])
+    else:
+        q = f16(np.abs(rng.normal(size=(T, 384))) + 0.5)
+        k = rng.normal(size=(T, 384))
+        k[T - 1] = 4.0
+        k = f16(k)
+    v = f16(rng.normal(size=(T, 384)))
+    out = allocf(eng, T, 384)
+    run(eng, K_ATTN, [1, grid, tpad],
+        [up(eng, head_major(q, 1, T, tpad)), up(eng, head_major(k, 1, T, tpad)),
+         up(eng, head_major(v, 1, T, tpad)), out])
+    y = readf(eng, out, T, 384)
+    ref = oracle.attention(q.astype(np.float64), k.astype(np.float64), v.astype(np.float64))
+    check(y, ref, atol=2.0**-9 * np.abs(v).max(), cos_min=0.9999, what=f"attention {case} T={T}")
+
+
 @pytest.mark.parametrize("rows,kdim", [(1, 384), (33, 1536), (1001, 384), (1001, 1536), (201, 1536), (12864, 384)])
 def test_resid(eng, rows, kdim):
     rng = np.random.default_rng(rows + kdim)
