@@ -342,6 +342,21 @@ __device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory")
 // of the N may be a DMA load issued after X: all register loads are issued
 // before the DMA loads they are waited with.
 
+// Calls f(integral_constant<int, I>) for I = 0 .. N-1.
+template <int N, int I = 0, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<N, I + 1>(f);
+    }
+}
+
+// No work between the stages of the K loop.
+struct NoMid {
+    template <class A>
+    __device__ __forceinline__ void operator()(A&, int) const {}
+};
+
 // The K loop with activations in registers (two sets, ActFrags) and the
 // weight stages moved into three LDS buffers by DMA (WeightDma). Step s
 // issues the activation loads of stage s+1 into the register set that held
@@ -357,9 +372,11 @@ __device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory")
 // DMA in flight. Nothing is loaded past the last stage. With KT > 0 the
 // stage count is KT, known at compile time, and the steps are fully unrolled
 // (any KT); otherwise k_tiles must be a multiple of 6 (the launchers check).
-template <class T, int KT = 0, class AL, class WD, class Settle>
+// mid(acc, s) runs in step s after its loads are issued and before its
+// MFMAs: additive work on the accumulators there issues beside the MFMAs.
+template <class T, int KT = 0, class AL, class WD, class Settle, class Mid = NoMid>
 __device__ __forceinline__ void gemm_main_dma(AL (&al)[2], const WD& wd, half_t* b0, half_t* b1, half_t* b2, int m0,
-                                              int n0, int k_tiles_rt, Acc<T>& acc, Settle&& settle) {
+                                              int n0, int k_tiles_rt, Acc<T>& acc, Settle&& settle, Mid&& mid = Mid{}) {
     const int k_tiles = KT > 0 ? KT : k_tiles_rt;
     static_assert(AL::kInRegs, "activations in registers");
     constexpr int NW = WD::PER_WAVE;
@@ -382,6 +399,7 @@ __device__ __forceinline__ void gemm_main_dma(AL (&al)[2], const WD& wd, half_t*
         if (s + 1 < k_tiles) next.load(m0, n0, s + 1, tid);
         compiler_fence();
         if (more) wd.load(fill, n0, s + 2, tid);
+        mid(acc, s);
         mma_stage_frag<T>(cur, tid, a, acc);
         if (more)
             vm_barrier<NW>();
@@ -405,16 +423,16 @@ __device__ __forceinline__ void gemm_main_dma(AL (&al)[2], const WD& wd, half_t*
 }
 
 // gemm_tile over gemm_main_dma.
-template <class T, int NS = 1, int KT = 0, class AL, class WD, class Issue, class Settle, class Epi>
+template <class T, int NS = 1, int KT = 0, class AL, class WD, class Issue, class Settle, class Epi, class Mid = NoMid>
 __device__ __forceinline__ void gemm_tile_dma(AL (&al)[2], WD& wd, half_t* b0, half_t* b1, half_t* b2, int n_tiles,
                                               int total_tiles, int k_tiles, Issue&& issue, Settle&& settle,
-                                              Epi&& epi) {
+                                              Epi&& epi, Mid&& mid = Mid{}) {
     const int t = NS == 1 ? xcd_tile(total_tiles) : xcd_tile_split<NS>(total_tiles / n_tiles, n_tiles);
     if (t < 0) return;  // uniform per workgroup
     const int n0 = (t % n_tiles) * T::BN, m0 = (t / n_tiles) * T::BM;
     issue(m0, n0);
     Acc<T> acc;
-    gemm_main_dma<T, KT>(al, wd, b0, b1, b2, m0, n0, k_tiles, acc, settle);
+    gemm_main_dma<T, KT>(al, wd, b0, b1, b2, m0, n0, k_tiles, acc, settle, mid);
     epi(acc, m0, n0);
 }
 

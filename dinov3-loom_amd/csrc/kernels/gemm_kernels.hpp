@@ -420,10 +420,6 @@ __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void swiglu_kernel(
                 for (int g = 0; g < 4; ++g) {
                     const int c = g * 8 + f.hi * 4, nl = f.n_base - n0 + 64 * q + c;
                     float4_t gate = group4(acc.v[2 * q][j], g), up = group4(acc.v[2 * q + 1][j], g);
-                    if constexpr (LN) {
-                        gate -= rn[j].mean * *(const float4_t*)&cst[1][nl];
-                        up -= rn[j].mean * *(const float4_t*)&cst[1][nl + 32];
-                    }
                     const float4_t gs = gate * sg + *(const float4_t*)&cst[0][nl];
                     const float4_t us = up * su + *(const float4_t*)&cst[0][nl + 32];
                     float4_t r;
@@ -436,6 +432,30 @@ __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void swiglu_kernel(
                     *(half8_t*)(p.act + ((size_t)mb * (kFF / 16) + f.n_base / 32 + 2 * q + kk) * 512 + lane * 8) =
                         frag_swap(y[2 * kk], y[2 * kk + 1]);
             }
+        }
+    },
+    // The folded LayerNorm's -mean * wsum, added to column block i of the
+    // accumulators at step i + 1 of the K loop (an additive term may join
+    // the sum at any point), where its FMAs issue beside the MFMAs instead
+    // of lengthening the epilogue.
+    [&](Acc<T>& acc, int s) {
+        if constexpr (LN) {
+            static_for<T::FN>([&](auto I) {
+                constexpr int i = decltype(I)::value;
+                if (s == i + 1) {
+                    const int hi = (threadIdx.x & 63) >> 5;
+                    float4_t w[4];
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) w[g] = *(const float4_t*)&cst[1][32 * i + 8 * g + 4 * hi];
+#pragma unroll
+                    for (int j = 0; j < T::FM; ++j)
+#pragma unroll
+                        for (int g = 0; g < 4; ++g)
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                acc.v[i][j][4 * g + e] = fmaf(-rn[j].mean, w[g][e], acc.v[i][j][4 * g + e]);
+                }
+            });
         }
     });
 }
