@@ -360,6 +360,7 @@ template <class T, bool LN>
 __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void swiglu_kernel(SwigluArgs p) {
     static_assert(T::TN % 64 == 0 && T::WGN == 1, "whole gate/up pairs, whole rows per wave");
     static_assert(T::BN <= T::THREADS, "one thread per column constant");
+    static_assert(kHidden / T::BK > T::FN, "a K-loop step for every column block's LayerNorm mean term");
     __shared__ __attribute__((aligned(16))) half_t wb0[T::WF_HALFS], wb1[T::WF_HALFS], wb2[T::WF_HALFS];
     __shared__ __attribute__((aligned(16))) float cst[2][T::BN];  // bias, wsum
     constexpr int NT = 2 * kFF / T::BN;
