@@ -20,7 +20,7 @@
 // cross-half exchange, and the running rescale of O^T is a per-lane scalar.
 // Q is scaled by 1/8 in registers and log2(e) is folded into one FMA per
 // score, so the softmax runs on v_exp_f32; the running max is updated lazily
-// (only when a block's weights against it sum past e^kLazy), which skips
+// (only when a block's weights against it sum past e^8), which skips
 // most rescales of O and, on the common path, the block max itself.
 // P is rounded to f16 for the PV product; the denominator keeps the fp32
 // weights (as in the reference, attention_online_f16_wmma_cf16.loom:195-216).
@@ -31,8 +31,9 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int QB = 128;                  // queries per workgroup
-constexpr float kLazy = 8.0f;            // running-max slack of the lazy rescaling (score units)
-constexpr float kLazySum = 2980.957987f; // e^kLazy: the largest weight sum that needs no rescale
+// The lazy rescaling's slack: the running max moves only when a block's
+// weights against it sum past e^8 (some score more than 8 above it).
+constexpr float kLazySum = 2980.957987f;  // e^8
 
 // LDS on gfx950 has 64 banks of 4 bytes: two 128-byte key rows per bank
 // cycle. Chunk c of key row r sits at slot c ^ swz_slot(r), with
@@ -105,11 +106,11 @@ __device__ __forceinline__ void attend32(QueryState& st, const half_t* sK, const
             if (key0 + 8 * (r >> 2) + 4 * hi + (r & 3) >= T) s[r] = neg_inf;
     }
     // Weights against the running max; the block max is needed only when
-    // some lane's weights sum past e^kLazy (a weight may then exceed it):
+    // some lane's weights sum past e^8 (a weight may then exceed it):
     // the first block of a walk (m_run starts at -1e30, so the sum is inf)
-    // and blocks whose scores grew by more than kLazy. Those lanes move
+    // and blocks whose scores grew by more than 8. Those lanes move
     // their max to the block's, rescale O and l, and recompute; every
-    // weight is then at most its sum, at most e^kLazy, well inside f16.
+    // weight is then at most its sum, at most e^8, well inside f16.
     float p[16];
     float mb = st.m_run * kLog2e;
     float sum = 0.f;
