@@ -293,6 +293,25 @@ def test_512_high_resolution(models, oracle_weights, preset):
     assert c_all > 0.9999 and c_cls > 0.9999
 
 
+@pytest.mark.parametrize("size", [64, 256, 384])
+def test_other_image_sizes(models, oracle_weights, size):
+    # Image sizes other than 224 and 512 (any multiple of 16 is accepted):
+    # 21, 261 and 581 tokens run the attention kernel with a run-time count
+    # of 64-key blocks, and the RoPE tables and patch gather of 4x4, 16x16
+    # and 24x24 grids. Stress preset against the oracle; each image of the
+    # batch of two equals it alone, bitwise.
+    G = size // 16
+    m = models(1, max_batch=2, image_size=size)
+    assert m.tokens == G * G + 5
+    px = d.random_pixels(size, 2, size)
+    out = m.forward(px)
+    assert out.shape == (2, G * G + 5, 384)
+    for i in range(2):
+        c_all, c_cls, _ = compare(out[i], oracle.forward(oracle_weights(1), px[i], G), f"{size}x{size} image {i}")
+        assert c_all > 0.9999 and c_cls > 0.9999
+    assert np.array_equal(m.forward(px[1:]), out[1:])
+
+
 def test_benchmark(models):
     m = models(0)
     px = d.random_pixels(1, 4)
