@@ -312,6 +312,17 @@ def test_other_image_sizes(models, oracle_weights, size):
     assert np.array_equal(m.forward(px[1:]), out[1:])
 
 
+def test_largest_image_size(models, oracle_weights):
+    # The largest accepted image, 1024x1024: 4096 patches + 5 = 4101 tokens
+    # (65 run-time key blocks per head, RoPE on the 64x64 grid).
+    m = models(1, max_batch=1, image_size=1024)
+    assert m.tokens == 4101
+    px = d.random_pixels(1024, 1, 1024)
+    out = m.forward(px)
+    c_all, c_cls, _ = compare(out[0], oracle.forward(oracle_weights(1), px[0], 64), "1024x1024")
+    assert c_all > 0.9999 and c_cls > 0.9999
+
+
 def test_benchmark(models):
     m = models(0)
     px = d.random_pixels(1, 4)
