@@ -293,12 +293,12 @@ def test_512_high_resolution(models, oracle_weights, preset):
     assert c_all > 0.9999 and c_cls > 0.9999
 
 
-@pytest.mark.parametrize("size", [64, 256, 384])
+@pytest.mark.parametrize("size", [16, 64, 256, 384])
 def test_other_image_sizes(models, oracle_weights, size):
     # Image sizes other than 224 and 512 (any multiple of 16 is accepted):
-    # 21, 261 and 581 tokens run the attention kernel with a run-time count
-    # of 64-key blocks, and the RoPE tables and patch gather of 4x4, 16x16
-    # and 24x24 grids. Stress preset against the oracle; each image of the
+    # 6 (the smallest: one patch), 21, 261 and 581 tokens run the attention
+    # kernel with a run-time count of 64-key blocks, and the RoPE tables and
+    # patch gather of 1x1, 4x4, 16x16 and 24x24 grids. Stress preset against the oracle; each image of the
     # batch of two equals it alone, bitwise.
     G = size // 16
     m = models(1, max_batch=2, image_size=size)
