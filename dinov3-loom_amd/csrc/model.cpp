@@ -446,7 +446,7 @@ private:
     uint64_t patches_ = 196, tokens_ = 201, tpad_ = 256, image_elems_ = 0;
     int splitk_ = 0;
     int fused_ln_ = 1;
-    uint32_t branches_ = 3;
+    uint32_t branches_ = 2;
     std::unique_ptr<dhx_engine, EngineFree> engine_;
     std::map<std::string, dhx_region> weights_;
     dhx_region a_[kBuffers];

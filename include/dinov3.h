@@ -122,7 +122,7 @@ int dinov3_set_splitk(dinov3_model *m, int mode);
 int dinov3_set_layernorm_fusion(dinov3_model *m, int on);
 /* Image groups run side by side (no reference counterpart): batches of at
  * least 4*n images are cut into n groups (1 <= n <= DHX_MAX_BRANCHES,
- * default 3) recorded as concurrent branches of one graph, so one group's
+ * default 2) recorded as concurrent branches of one graph, so one group's
  * kernels fill the last partial wave of workgroups of the other's. Results
  * are bitwise the same for every n. Graphs are kept per (batch, variant). */
 int dinov3_set_branches(dinov3_model *m, uint32_t n);
