@@ -76,7 +76,12 @@ __device__ __forceinline__ int tr_col_of(int lane) { return 16 * ((lane >> 4) & 
 // One sub-block of 32 keys (rows row0 .. row0+31 of the swizzled K and V
 // blocks in LDS, keys key0 .. key0+31 of the sequence of T):
 // S^T = K Q^T, masked past T, lazy running max, P = 2^(s log2e - m log2e),
-// O^T += V^T P^T with P in f16 and the denominator in f32.
+// O^T += V^T P^T with P in f16 and the denominator in f32. FIRST: the first
+// sub-block of a walk (O and l still zero), whose weights against the
+// initial max of -1e30 would all overflow: its block max becomes the
+// running max directly, with one pass of exponentials instead of two (the
+// same values and rounding as the rescale path).
+template <bool FIRST = false>
 __device__ __forceinline__ void attend32(QueryState& st, const half_t* sK, const half_t* sV, int row0, int key0,
                                          int T, int lane) {
     const int l32 = lane & 31, hi = lane >> 5;
@@ -105,41 +110,45 @@ __device__ __forceinline__ void attend32(QueryState& st, const half_t* sK, const
         for (int r = 0; r < 16; ++r)
             if (key0 + 8 * (r >> 2) + 4 * hi + (r & 3) >= T) s[r] = neg_inf;
     }
-    // Weights against the running max; the block max is needed only when
-    // some lane's weights sum past e^8 (a weight may then exceed it):
-    // the first block of a walk (m_run starts at -1e30, so the sum is inf)
-    // and blocks whose scores grew by more than 8. Those lanes move
-    // their max to the block's, rescale O and l, and recompute; every
-    // weight is then at most its sum, at most e^8, well inside f16.
+    // Weights against the running max; after the first sub-block (which
+    // takes its own max), the block max is needed only when some lane's
+    // weights sum past e^8 (a weight may then exceed it): blocks whose
+    // scores grew by more than 8. Those lanes move their max to the
+    // block's, rescale O and l, and recompute; every weight is then at most
+    // its sum, at most e^8, well inside f16.
     float p[16];
-    float mb = st.m_run * kLog2e;
-    float sum = 0.f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        p[r] = fast_exp2(fmaf(s[r], kLog2e, -mb));
-        sum += p[r];
-    }
-    sum = half_pair_sum(sum);
-    const bool grow = !(sum <= kLazySum);  // also true for inf (first block)
-    if (__any(grow)) {  // uniform across the wave
-        float mx = s[0];
-#pragma unroll
-        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
-        mx = half_pair_max(mx);  // every sub-block holds a valid key of each pair
-        const float m_new = grow ? fmaxf(mx, st.m_run) : st.m_run;
-        const float alpha = fast_exp2((st.m_run - m_new) * kLog2e);
-        st.l_run *= alpha;
-        st.o[0] *= alpha;
-        st.o[1] *= alpha;
-        st.m_run = m_new;
-        mb = m_new * kLog2e;
-        sum = 0.f;
+    auto weights = [&](float m) {  // p = 2^(s log2e - m log2e); the pair's sum
+        const float mb = m * kLog2e;
+        float sum = 0.f;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             p[r] = fast_exp2(fmaf(s[r], kLog2e, -mb));
             sum += p[r];
         }
-        sum = half_pair_sum(sum);
+        return half_pair_sum(sum);
+    };
+    auto block_max = [&] {
+        float mx = s[0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
+        return half_pair_max(mx);  // every sub-block holds a valid key of each pair
+    };
+    float sum;
+    if constexpr (FIRST) {
+        st.m_run = block_max();
+        sum = weights(st.m_run);
+    } else {
+        sum = weights(st.m_run);
+        const bool grow = !(sum <= kLazySum);
+        if (__any(grow)) {  // uniform across the wave
+            const float m_new = grow ? fmaxf(block_max(), st.m_run) : st.m_run;
+            const float alpha = fast_exp2((st.m_run - m_new) * kLog2e);
+            st.l_run *= alpha;
+            st.o[0] *= alpha;
+            st.o[1] *= alpha;
+            st.m_run = m_new;
+            sum = weights(m_new);
+        }
     }
     st.l_run += sum;
     // P^T as the b operand: k-slice element j of this lane is key
@@ -271,7 +280,10 @@ __global__ __launch_bounds__(kThreads, 3) void attention_kernel(AttentionArgs p)
         for (int sub = 0; sub < KBT::KB / 32 && active; ++sub) {
             const int key0 = kb * KBT::KB + sub * 32;
             if (key0 >= T) break;  // uniform across the workgroup
-            attend32(st, sK, sV, sub * 32, key0, T, lane);
+            if (NKB > 0 && kb == 0 && sub == 0)  // the unrolled walk: its first block is known at compile time
+                attend32<true>(st, sK, sV, 0, key0, T, lane);
+            else
+                attend32(st, sK, sV, sub * 32, key0, T, lane);
         }
     };
     // Block kb is computed from buffer kb % 3 while the DMA of block kb+2
@@ -366,7 +378,12 @@ __device__ __forceinline__ void split_walk(QueryState& st, half_t* const (&kbuf)
     for (int s = 0; s < NH; ++s) {
         if (s + 2 < NH) dma((s + 2) % 3, s + 2);
         const int kb = first + s;
-        if (active && kb < nkb) attend32(st, kbuf[s % 3], vbuf[s % 3], 0, kb * 32, T, lane);
+        if (active && kb < nkb) {
+            if (s == 0)
+                attend32<true>(st, kbuf[0], vbuf[0], 0, kb * 32, T, lane);
+            else
+                attend32(st, kbuf[s % 3], vbuf[s % 3], 0, kb * 32, T, lane);
+        }
         if (s + 2 < NH)
             vm_barrier<2>();
         else
@@ -374,8 +391,10 @@ __device__ __forceinline__ void split_walk(QueryState& st, half_t* const (&kbuf)
     }
 }
 
+// Two workgroups per CU: four waves per SIMD (the bound below), which caps
+// the kernel at 128 VGPRs; one register more halves the resident workgroups.
 template <int NH>
-__global__ __launch_bounds__(kSplitThreads, 2) void attention_split_kernel(AttentionArgs p) {
+__global__ __launch_bounds__(kSplitThreads, 4) void attention_split_kernel(AttentionArgs p) {
     // Per half three K and three V blocks of 4 KB (48 KB), as separate
     // variables (the compiler tells distinct variables apart, not the rows of
     // one array); reused at the end for the merge.
