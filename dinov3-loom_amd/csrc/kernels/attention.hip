@@ -4,7 +4,9 @@
 // One workgroup = 4 waves = 128 queries of one (image, head); each wave owns
 // 32 queries. Keys stream through LDS in blocks of 32 or 64 (K and V both as
 // [key][ch]), so the same kernel serves 201 tokens (224x224) and 1029
-// tokens (512x512). The blocks move from global memory straight into three
+// tokens (512x512). q, k and v come per (image, head) as [tpad][64]
+// matrices in fragment order (a wave's Q fragments are then 1 KB contiguous
+// loads). The blocks move from global memory straight into three
 // LDS buffers with DMA loads (buffer_load ... lds), two blocks ahead; each
 // 128-byte key row is stored with its 16-byte chunks XOR-swizzled by the
 // row (swz below), so the row reads of K and the transpose reads of V hit
@@ -195,12 +197,19 @@ struct KeyBlock {
     static constexpr int LOADS = KB / 32;          // DMA loads of 8 rows per matrix and wave
 };
 
-// DMA offsets of this lane for moving 8 key rows (one 1 KB load): lane i
-// lands at LDS slot (row i/8, chunk slot i%8) of rows r0 .. r0+7 and fetches
-// the chunk the swizzle puts there (r0 % 8 == 0, so row % 16 = r0 % 16 + i/8).
+// DMA offsets for moving 8 key rows (one 1 KB load) out of a
+// fragment-order [tpad][64] matrix: lane i lands at LDS slot (row i/8, chunk
+// slot i%8) of rows r0 .. r0+7 and fetches the chunk c the swizzle puts
+// there (r0 % 8 == 0, so row % 16 = r0 % 16 + i/8). Chunk c (channels 8c ..
+// 8c+7) of row r sits at byte ((r/32)*4 + c/2)*1024 + ((c%2)*32 + r%32)*16:
+// the lane part holds c and i/8, the scalar part (dma_row_offset) r0's
+// 32-row block and r0 % 32 (no carry: r0 % 32 + 7 < 32). A load reads 8
+// runs of 128 bytes (8 rows of one chunk each).
 __device__ __forceinline__ int dma_lane_offset(int lane, int r0) {
-    return (lane >> 3) * 128 + (((lane & 7) ^ swz_slot(r0 % 16 + (lane >> 3))) << 4);
+    const int c = (lane & 7) ^ swz_slot(r0 % 16 + (lane >> 3));
+    return ((c >> 1) << 10) + ((c & 1) << 9) + (lane >> 3) * 16;
 }
+__device__ __forceinline__ int dma_row_offset(int r0) { return (r0 >> 5) * 4096 + (r0 & 31) * 16; }
 
 template <int NKB>
 __global__ __launch_bounds__(kThreads, 3) void attention_kernel(AttentionArgs p) {
@@ -238,7 +247,7 @@ __global__ __launch_bounds__(kThreads, 3) void attention_kernel(AttentionArgs p)
     auto dma = [&](half_t* k_buf, half_t* v_buf, int kb) {
 #pragma unroll
         for (int j = 0; j < KBT::LOADS; ++j) {
-            const int row = wave * (KBT::KB / 4) + j * 8, soff = (kb * KBT::KB + row) * 128;
+            const int row = wave * (KBT::KB / 4) + j * 8, soff = dma_row_offset(kb * KBT::KB + row);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(k_buf + row * kHeadDim),
                                                      16, voff[j], soff, 0, 0);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)(v_buf + row * kHeadDim),
@@ -257,7 +266,7 @@ __global__ __launch_bounds__(kThreads, 3) void attention_kernel(AttentionArgs p)
     QueryState st;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
-        st.qf[kk] = *(const half8_t*)(qg + (size_t)min(qrow, T - 1) * kHeadDim + kk * 16 + hi * 8);
+        st.qf[kk] = *(const half8_t*)(qg + frag_piece(min(qrow, T - 1), kk * 16 + hi * 8, kHeadDim));
     asm volatile("" ::: "memory");
     if (NKB == 0 || nkb > 1) {  // with a runtime count, block 1 repeats block 0 when there is one block
         dma(sK1, sV1, min(1, nkb - 1));
@@ -353,7 +362,7 @@ __device__ __forceinline__ void split_walk(QueryState& st, half_t* const (&kbuf)
     const int hi = lane >> 5;
     const int voff = dma_lane_offset(lane, 8 * hwave), last = min(first + NH, nkb) - 1;
     auto dma = [&](int buf, int s) {
-        const int kb = min(first + s, last), row = 8 * hwave, soff = (kb * 32 + row) * 128;
+        const int kb = min(first + s, last), row = 8 * hwave, soff = dma_row_offset(kb * 32 + row);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(kbuf[buf] + row * kHeadDim),
                                                  16, voff, soff, 0, 0);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)(vbuf[buf] + row * kHeadDim),
@@ -364,7 +373,7 @@ __device__ __forceinline__ void split_walk(QueryState& st, half_t* const (&kbuf)
     dma(0, 0);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
-        st.qf[kk] = *(const half8_t*)(qg + (size_t)min(qrow, T - 1) * kHeadDim + kk * 16 + hi * 8);
+        st.qf[kk] = *(const half8_t*)(qg + frag_piece(min(qrow, T - 1), kk * 16 + hi * 8, kHeadDim));
     asm volatile("" ::: "memory");
     dma(1, 1);
     vm_barrier<2>();

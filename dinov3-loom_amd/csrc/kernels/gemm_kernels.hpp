@@ -144,8 +144,11 @@ __device__ __forceinline__ void init_frags(ActFrags<T> (&al)[2], const half_t* a
 // both use angle column c of the RoPE tables (DINOv3's tables repeat columns
 // 0..31 in 32..63; only the first half is read). Results are rounded to f16
 // and regrouped in registers (frag_swap) so each lane holds 8 consecutive
-// channels of its row, written as 16-byte pieces of the head rows: q, k and
-// v are all head-major [image][head][tpad][64].
+// channels of its row. q, k and v are [image][head] matrices of tpad rows x
+// 64 channels, each in fragment order: a lane's 8 channels are one 16-byte
+// piece of a fragment, so the 64 lanes of a store cover one or two runs of
+// whole rows' pieces per half-fragment (a row-major head row would take 32
+// separate 32-byte writes per store instead).
 template <class T, bool LN>
 __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void qkv_rope_kernel(QkvArgs p) {
     static_assert(T::TN == 2 * kHeadDim && T::WGN == 1, "two heads per wave, whole rows per wave");
@@ -251,12 +254,12 @@ __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void qkv_rope_kerne
                 // Channels 16kk + 8hi .. +7 of the head for kk = 0..3.
                 const half8_t c0 = frag_swap(lo_h[0], lo_h[1]), c1 = frag_swap(lo_h[2], lo_h[3]);
                 const half8_t c2 = frag_swap(up_h[0], up_h[1]), c3 = frag_swap(up_h[2], up_h[3]);
-                half_t* const row = out + (((size_t)img * kHeads + head0 + h2) * p.tpad + tok) * kHeadDim + f.hi * 8;
+                half_t* const hm = out + ((size_t)img * kHeads + head0 + h2) * p.tpad * kHeadDim;
                 if (mr < M) {
-                    *(half8_t*)(row) = c0;
-                    *(half8_t*)(row + 16) = c1;
-                    *(half8_t*)(row + 32) = c2;
-                    *(half8_t*)(row + 48) = c3;
+                    *(half8_t*)(hm + frag_piece(tok, f.hi * 8, kHeadDim)) = c0;
+                    *(half8_t*)(hm + frag_piece(tok, 16 + f.hi * 8, kHeadDim)) = c1;
+                    *(half8_t*)(hm + frag_piece(tok, 32 + f.hi * 8, kHeadDim)) = c2;
+                    *(half8_t*)(hm + frag_piece(tok, 48 + f.hi * 8, kHeadDim)) = c3;
                 }
             }
         }

@@ -50,8 +50,9 @@ constexpr int kStatSlots = kHidden / 64;
 constexpr int kStatFloats = 2 * kStatSlots;
 
 // h [rows][384] frag . Wqkv[1152][384]^T + b, 2D RoPE on q and k of patch
-// tokens, written head-major: q, k, v [images][6][tpad][64] (rows past the
-// image's tokens are never written). cos / sin are [patches][64] with columns
+// tokens, written per (image, head): q, k, v [images][6] matrices of
+// [tpad][64] in fragment order (rows past the image's tokens are never
+// written). cos / sin are [patches][64] with columns
 // 32..63 repeating 0..31 (the rotation of channels c and c+32 uses angle c);
 // only columns 0..31 are read.
 // With stats == nullptr: h = LN1(x) is given and out = h.W^T + bias. With
@@ -136,7 +137,8 @@ struct ReduceArgs {
     float* stats = nullptr;  // optional: row statistics of the updated x
 };
 
-// Rows tokens .. tpad-1 of q, k and v [images][6][tpad][64] set to zero:
+// Rows tokens .. tpad-1 of q, k and v ([images][6] fragment-order [tpad][64]
+// matrices) set to zero:
 // attention reads them as masked keys, so they must be finite. For buffers
 // that did not come zeroed from the engine (the allocation-free forward's
 // scratch, which keeps earlier calls' data). A fill kernel, not a memset, so

@@ -149,7 +149,7 @@ __global__ __launch_bounds__(kThreads) void zero_pad_rows_kernel(PadRowsArgs p) 
     const size_t ih = j / ((size_t)pad * 8);  // image * heads + head
     const int row = p.tokens + (int)(j / 8 % pad), piece = (int)(j % 8);
     half_t* const base = t == 0 ? p.q : t == 1 ? p.k : p.v;
-    *(half8_t*)(base + (ih * p.tpad + row) * kHeadDim + piece * 8) = half8_t{};
+    *(half8_t*)(base + ih * p.tpad * kHeadDim + frag_piece(row, piece * 8, kHeadDim)) = half8_t{};
 }
 
 }  // namespace

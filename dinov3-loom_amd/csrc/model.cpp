@@ -155,8 +155,8 @@ public:
         // Activations in fragment order: each image group starts on a 32-row
         // block, so up to 32 padding rows per group.
         const uint64_t rf = r + 32ull * DHX_MAX_BRANCHES;
-        // x, h, attn and act are f16 in fragment order; q/k/v are f16 head-major (padded rows
-        // stay zero); out, the NCHW images, the split-K slabs and the
+        // x, h, attn and act are f16 in fragment order, and so is each
+        // (image, head) [tpad][64] matrix of q/k/v (padded rows stay zero); out, the NCHW images, the split-K slabs and the
         // LayerNorm row statistics of x are f32. The images and out exist
         // twice (one per transfer slot) so that consecutive chunks of a
         // forward overlap their uploads and readbacks with each other's graph.

@@ -69,9 +69,10 @@ typedef struct dhx_region {
  * and split-K GEMMs (qkv_w, qkv_wln, w [384][k], gateup_w, gateup_wln) are in
  * the same fragment order (their row counts are multiples of 32): the kernels
  * move them into LDS block by block with DMA loads.
- * q, k and v are [images][6][tpad][64] f16 (rows T .. tpad-1 are never
- * written and must hold finite values for attention: regions from
- * dhx_allocate start zeroed), tpad a multiple of 128 >= T = grid*grid + 5;
+ * q, k and v are [images][6] f16 matrices of [tpad][64], each in the same
+ * fragment order with K = 64 (rows T .. tpad-1 are never written and must
+ * hold finite values for attention: regions from dhx_allocate start zeroed),
+ * tpad a multiple of 128 >= T = grid*grid + 5;
  * the RoPE tables hold one row of 64 angles per patch whose columns 32..63
  * repeat 0..31 (as DINOv3's do); the kernels read columns 0..31; k (and k / splits) a multiple
  * of 384 (the GEMM K loop runs stages of 64 six at a time). Every binding's size is

@@ -214,6 +214,18 @@ def head_major(x, images, T, tpad):
     return out
 
 
+def heads_frag(x, images, T, tpad):
+    """[images*T, 384] -> the kernels' q/k/v layout: every (image, head)
+    [tpad][64] matrix (zero padding rows) in fragment order."""
+    return to_frag(head_major(x, images, T, tpad).reshape(-1, 64))
+
+
+def read_heads(e, region, images, tpad):
+    """q/k/v as the kernels write them -> [images, 6, tpad, 64]."""
+    n = images * 6 * tpad
+    return from_frag(e.read(region, np.float16, (n * 64,)), n, 64).reshape(images, 6, tpad, 64)
+
+
 @pytest.mark.parametrize("images,grid", [(3, 14), (1, 32), (2, 4)])
 def test_qkv_rope(eng, images, grid):
     rng = np.random.default_rng(7 + grid)
@@ -232,9 +244,9 @@ def test_qkv_rope(eng, images, grid):
     nb = images * 6 * tpad * 64 * 2
     q, k, v = eng.allocate(nb), eng.allocate(nb), eng.allocate(nb)
     run(eng, K_QKV, [images, grid, tpad], [upf(eng, h), upf(eng, w), up(eng, b), up(eng, cos), up(eng, sin), q, k, v])
-    gq = eng.read(q, np.float16, (images, 6, tpad, 64))
-    gk = eng.read(k, np.float16, (images, 6, tpad, 64))
-    gv = eng.read(v, np.float16, (images, 6, tpad, 64))
+    gq = read_heads(eng, q, images, tpad)
+    gk = read_heads(eng, k, images, tpad)
+    gv = read_heads(eng, v, images, tpad)
     hd = h.astype(np.float64)
     for i in range(images):
         rows = hd[i * T:(i + 1) * T]
@@ -259,8 +271,8 @@ def test_attention(eng, images, grid, qscale):
     v = f16(rng.normal(size=(images * T, 384)))
     out = allocf(eng, images * T, 384)
     run(eng, K_ATTN, [images, grid, tpad],
-        [up(eng, head_major(q, images, T, tpad)), up(eng, head_major(k, images, T, tpad)),
-         up(eng, head_major(v, images, T, tpad)), out])
+        [up(eng, heads_frag(q, images, T, tpad)), up(eng, heads_frag(k, images, T, tpad)),
+         up(eng, heads_frag(v, images, T, tpad)), out])
     y = readf(eng, out, images * T, 384)
     for i in range(images):
         sl = slice(i * T, (i + 1) * T)
@@ -290,8 +302,8 @@ def test_attention_running_max_moves(eng, case, grid):
     v = f16(rng.normal(size=(T, 384)))
     out = allocf(eng, T, 384)
     run(eng, K_ATTN, [1, grid, tpad],
-        [up(eng, head_major(q, 1, T, tpad)), up(eng, head_major(k, 1, T, tpad)),
-         up(eng, head_major(v, 1, T, tpad)), out])
+        [up(eng, heads_frag(q, 1, T, tpad)), up(eng, heads_frag(k, 1, T, tpad)),
+         up(eng, heads_frag(v, 1, T, tpad)), out])
     y = readf(eng, out, T, 384)
     ref = oracle.attention(q.astype(np.float64), k.astype(np.float64), v.astype(np.float64))
     check(y, ref, atol=2.0**-9 * np.abs(v).max(), cos_min=0.9999, what=f"attention {case} T={T}")
@@ -480,8 +492,8 @@ def test_qkv_rope_layernorm_fused(eng, images, grid, offset):
     run(eng, K_QKV_LN, [images, grid, tpad],
         [upf(eng, x), up(eng, slot_stats(x)), upf(eng, wl), up(eng, wsum), up(eng, t), up(eng, cos), up(eng, sin),
          q, k, v])
-    gq = eng.read(q, np.float16, (images, 6, tpad, 64))
-    gv = eng.read(v, np.float16, (images, 6, tpad, 64))
+    gq = read_heads(eng, q, images, tpad)
+    gv = read_heads(eng, v, images, tpad)
     h = oracle.layernorm(x.astype(np.float64), gamma, beta)  # LN(x), unrounded
     for i in range(images):
         rows = h[i * T:(i + 1) * T]
@@ -558,8 +570,8 @@ def test_qkv_rope_layernorm_fused_adversarial(eng, case):
     to_tok = lambda a, i: a[i, :, :T].transpose(1, 0, 2).reshape(T, 384)
     for part, lo in (("q", 0), ("v", 768)):
         idx = 0 if part == "q" else 2
-        gf = eng.read(qkv_f[idx], np.float16, (images, 6, tpad, 64))
-        gu = eng.read(qkv_u[idx], np.float16, (images, 6, tpad, 64))
+        gf = read_heads(eng, qkv_f[idx], images, tpad)
+        gu = read_heads(eng, qkv_u[idx], images, tpad)
         for i in range(images):
             ref = oracle.linear(h[i * T:(i + 1) * T], w[lo:lo + 384].astype(np.float64), b[lo:lo + 384])
             if part == "q":
@@ -702,7 +714,7 @@ def test_attention_bitwise_repeatable(eng, shape):
     rng = np.random.default_rng(12)
     T = grid * grid + 5
     tpad = (T + 127) // 128 * 128
-    ins = [up(eng, head_major(f16(rng.normal(size=(images * T, 384)) * s), images, T, tpad)) for s in (2.0, 1.0, 1.0)]
+    ins = [up(eng, heads_frag(f16(rng.normal(size=(images * T, 384)) * s), images, T, tpad)) for s in (2.0, 1.0, 1.0)]
 
     def once():
         out = allocf(eng, images * T, 384)
