@@ -168,8 +168,12 @@ __device__ __forceinline__ void attend32(QueryState& st, const half_t* sK, const
 
 // Output of one lane's query: O / l in f16 into out (fragment order): each
 // 16-channel half of a 32-channel block becomes one 8-channel piece per lane
-// after frag_swap.
-__device__ __forceinline__ void store_query(const QueryState& st, half_t* out, int row, int head, int hi) {
+// after frag_swap. row0: the first query row of the wave (wave-uniform); the
+// wave's 32 rows lie in its 32-row block and the next, which the
+// write-through descriptor covers.
+__device__ __forceinline__ void store_query(const QueryState& st, half_t* out, int row0, int row, int head, int hi) {
+    const size_t base = (size_t)(row0 / 32) * (kHidden / 16) * 512;
+    const WtOut o(out + base, 2 * (kHidden / 16) * 1024);
     const float inv = 1.0f / st.l_run;
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct)
@@ -182,7 +186,7 @@ __device__ __forceinline__ void store_query(const QueryState& st, half_t* out, i
                                 (half_t)(a[8 * kk + 6] * inv), (half_t)(a[8 * kk + 7] * inv)};
             const half8_t piece = frag_swap(g0, g1);
             const int c = head * kHeadDim + ct * 32 + kk * 16 + hi * 8;
-            *(half8_t*)(out + frag_piece(row, c, kHidden)) = piece;
+            o.store((uint32_t)(frag_piece(row, c, kHidden) - base) * 2, piece);
         }
 }
 
@@ -333,7 +337,7 @@ __global__ __launch_bounds__(kThreads, 3) void attention_kernel(AttentionArgs p)
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
 
-    if (qrow < T) store_query(st, p.out, img * T + qrow, head, hi);
+    if (qrow < T) store_query(st, p.out, img * T + qb * QB + wave * 32, img * T + qrow, head, hi);
 }
 
 // Long sequences (512x512: 1029 tokens): each workgroup of 8 waves holds 128
@@ -467,7 +471,7 @@ __global__ __launch_bounds__(kSplitThreads, 4) void attention_split_kernel(Atten
         st.o[0][r] = st.o[0][r] * a0 + *slot(2 + r) * a1;
         st.o[1][r] = st.o[1][r] * a0 + *slot(18 + r) * a1;
     }
-    store_query(st, p.out, img * T + qrow, head, hi);
+    store_query(st, p.out, img * T + qb * QB + qw * 32, img * T + qrow, head, hi);
 }
 
 }  // namespace

@@ -28,6 +28,35 @@ constexpr float kLn2 = 0.6931471805599453f;
 // index stride.
 constexpr int kBufferRsrcWord3 = 0x00020000;
 
+// Output stores that write through the L2: 16-byte buffer stores with the
+// sc1 cache policy. On this multi-XCD GPU every dispatch ends by writing its
+// dirty L2 lines back (the XCDs' L2s are not coherent with each other), and
+// for a kernel that writes tens of MB that flush is a serial tail after its
+// last workgroup; written through, the lines are already out when the
+// kernel's waves finish. The descriptor covers `bytes` from `base`; both
+// must be wave-uniform (they are read from the first lane, so that the
+// descriptor lives in scalar registers: one the compiler cannot prove
+// uniform costs a loop over the lanes' values at every store). Offsets are
+// bytes from base.
+struct WtOut {
+    __amdgpu_buffer_rsrc_t r;
+    __device__ __forceinline__ WtOut(const void* base, uint32_t bytes) {
+        // readfirstlane returns int: each word goes back through uint32_t, or
+        // a low word with bit 31 set would sign-extend over the high word.
+        const uint64_t a = (uint64_t)(uintptr_t)base;
+        const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a);
+        const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+        r = __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)((hi << 32) | lo), 0,
+                                              (int)__builtin_amdgcn_readfirstlane(bytes), kBufferRsrcWord3);
+    }
+    template <class V>
+    __device__ __forceinline__ void store(uint32_t byte_off, V v) const {
+        static_assert(sizeof(V) == 16, "16-byte stores");
+        constexpr int kSc1 = 16;  // cache-policy bit SC1 of gfx940-family buffer instructions
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(uint4_t, v), r, (int)byte_off, 0, kSc1);
+    }
+};
+
 // v_mfma_f32_32x32x16_f16. Operand a: lane l holds row (l % 32), k-slice
 // 8*(l / 32) .. +7; operand b: lane l holds column (l % 32), the same
 // k-slice. The 16 results of lane l are rows 8*(r/4) + 4*(l/32) + r%4,

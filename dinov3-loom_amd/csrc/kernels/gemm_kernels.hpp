@@ -99,11 +99,16 @@ __global__ __launch_bounds__(T::THREADS) void patch_embed_kernel(PatchEmbedArgs 
         const int m = f.m_base + f.l32;
         const bool valid = m < M;
         const size_t row = valid ? (size_t)m + (size_t)(m / P + 1) * kPrefix : 0;  // image*Tok + kPrefix + patch
+        // The wave's 32 patch rows land in x rows row(m_base) .. at most
+        // 32 + 5 * (32 / P + 1) rows further: within 8 row blocks.
+        const size_t rb0 = ((size_t)f.m_base + (size_t)(f.m_base / P + 1) * kPrefix) / 32;
+        const WtOut xo(p.x + rb0 * (kHidden / 16) * 512, 8 * (kHidden / 16) * 1024);
         float v[32];
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             const half8_t h = *(const half8_t*)(st + f.l32 * SP + ks * 16 + f.hi * 8);
-            if (valid) *(half8_t*)(p.x + frag_piece((int)row, f.n_base + ks * 16 + f.hi * 8, kHidden)) = h;
+            if (valid)
+                xo.store((uint32_t)(frag_piece((int)row, f.n_base + ks * 16 + f.hi * 8, kHidden) - rb0 * (kHidden / 16) * 512) * 2, h);
 #pragma unroll
             for (int e = 0; e < 8; ++e) v[ks * 8 + e] = (float)h[e];
         }
@@ -222,6 +227,13 @@ __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void qkv_rope_kerne
         const Frag<T> f(m0, n0);
         const int part = f.n_base / kHidden, head0 = (f.n_base % kHidden) / kHeadDim;
         half_t* const out = part == 0 ? p.q : part == 1 ? p.k : p.v;
+        const size_t head_elems = (size_t)p.tpad * kHeadDim;
+        // The tile's rows lie in images img0 .. img0 + BM / Tok + 1 (img0
+        // from the tile origin, so it is uniform); the descriptor covers
+        // those.
+        const int img0 = min(m0, M - 1) / Tok;
+        const int span = min(p.images - img0, T::BM / Tok + 2);
+        const WtOut wo(out + (size_t)img0 * kHeads * head_elems, (uint32_t)(span * kHeads * head_elems * 2));
 #pragma unroll
         for (int j = 0; j < T::FM; ++j) {
             const int mr = f.row(j);
@@ -254,12 +266,12 @@ __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void qkv_rope_kerne
                 // Channels 16kk + 8hi .. +7 of the head for kk = 0..3.
                 const half8_t c0 = frag_swap(lo_h[0], lo_h[1]), c1 = frag_swap(lo_h[2], lo_h[3]);
                 const half8_t c2 = frag_swap(up_h[0], up_h[1]), c3 = frag_swap(up_h[2], up_h[3]);
-                half_t* const hm = out + ((size_t)img * kHeads + head0 + h2) * p.tpad * kHeadDim;
+                const uint32_t hm = (uint32_t)(((img - img0) * kHeads + head0 + h2) * head_elems) * 2;
                 if (mr < M) {
-                    *(half8_t*)(hm + frag_piece(tok, f.hi * 8, kHeadDim)) = c0;
-                    *(half8_t*)(hm + frag_piece(tok, 16 + f.hi * 8, kHeadDim)) = c1;
-                    *(half8_t*)(hm + frag_piece(tok, 32 + f.hi * 8, kHeadDim)) = c2;
-                    *(half8_t*)(hm + frag_piece(tok, 48 + f.hi * 8, kHeadDim)) = c3;
+                    wo.store(hm + (uint32_t)frag_piece(tok, f.hi * 8, kHeadDim) * 2, c0);
+                    wo.store(hm + (uint32_t)frag_piece(tok, 16 + f.hi * 8, kHeadDim) * 2, c1);
+                    wo.store(hm + (uint32_t)frag_piece(tok, 32 + f.hi * 8, kHeadDim) * 2, c2);
+                    wo.store(hm + (uint32_t)frag_piece(tok, 48 + f.hi * 8, kHeadDim) * 2, c3);
                 }
             }
         }
@@ -417,6 +429,7 @@ __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void swiglu_kernel(
             const int mb = f.m_base / 32 + j;
             if (mb >= mblocks) break;  // uniform per wave
             const float sg = rn[j].rstd * -kLog2e, su = rn[j].rstd * -kLn2;
+            const WtOut act(p.act + (size_t)mb * (kFF / 16) * 512, 32 * kFF * 2);
 #pragma unroll
             for (int q = 0; q < T::FN / 2; ++q) {
                 half4_t y[4];
@@ -433,8 +446,7 @@ __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void swiglu_kernel(
                 }
 #pragma unroll
                 for (int kk = 0; kk < 2; ++kk)
-                    *(half8_t*)(p.act + ((size_t)mb * (kFF / 16) + f.n_base / 32 + 2 * q + kk) * 512 + lane * 8) =
-                        frag_swap(y[2 * kk], y[2 * kk + 1]);
+                    act.store(((f.n_base / 32 + 2 * q + kk) * 512 + lane * 8) * 2, frag_swap(y[2 * kk], y[2 * kk + 1]));
             }
         }
     },

@@ -71,18 +71,19 @@ __global__ __launch_bounds__(kThreads) void layernorm_kernel(LayerNormArgs p) {
             half8_t h;
 #pragma unroll
             for (int e = 0; e < 8; ++e) h[e] = (half_t)y[e];
-            *(half8_t*)((half_t*)p.out + ((size_t)mb * kKs + ks) * 512 + lane * 8) = h;
+            const WtOut out((half_t*)p.out + (size_t)mb * kKs * 512, kKs * 1024);
+            out.store((ks * 512 + lane * 8) * 2, h);
         }
     }
     if (!p.f32_out) return;
     wave_lds_sync();
     // The wave's 32 rows x 96 columns: 24 float4 per row, 12 per lane.
     constexpr int Q = kLnKs * 4;  // float4 per row
+    const WtOut out((float*)p.out + (size_t)mb * 32 * kHidden, 32 * kHidden * 4);
 #pragma unroll
     for (int it = 0; it < 32 * Q / 64; ++it) {
         const int idx = it * 64 + lane, r = idx / Q, q = idx % Q, m = mb * 32 + r;
-        if (m < p.rows)
-            *(float4_t*)((float*)p.out + (size_t)m * kHidden + ks0 * 16 + q * 4) = *(const float4_t*)(st + r * kOutPitch + q * 4);
+        if (m < p.rows) out.store((r * kHidden + ks0 * 16 + q * 4) * 4, *(const float4_t*)(st + r * kOutPitch + q * 4));
     }
 }
 
