@@ -17,7 +17,7 @@ using PatchTile = Tile<64, 128, 2, 2>;
 using QkvTile = Tile<128, 128, 4, 1>;
 using ResidTile = Tile<128, 64, 4, 1>;
 using ResidTileK = Tile<128, 64, 4, 1, 128>;  // down projection (k = 1536)
-using SwigluTile = Tile<256, 128, 4, 1, 32>;
+using SwigluTile = Tile<256, 128, 4, 1, 64>;
 using SplitTile = Tile<128, 128, 4, 1>;
 
 template <class T, class Args>
