@@ -18,6 +18,10 @@ using QkvTile = Tile<128, 128, 4, 1>;
 using ResidTile = Tile<128, 64, 4, 1>;
 using ResidTileK = Tile<128, 64, 4, 1, 128>;  // down projection (k = 1536)
 using SwigluTile = Tile<256, 128, 4, 1, 64>;
+// SwiGLU for launches of fewer rows (batch 32 as two image groups, small
+// batches): 128-row tiles, three workgroups per CU instead of two.
+using SwigluTileS = Tile<128, 128, 4, 1, 64>;
+constexpr int kSwigluSmallRows = 4096;
 using SplitTile = Tile<128, 128, 4, 1>;
 
 template <class T, class Args>
@@ -63,13 +67,17 @@ hipError_t launch_resid(const ResidArgs& a, hipStream_t s) {
                    : launch<ResidTile>(gemm::resid_kernel<ResidTile, false>, tiles, a, s);
 }
 
-hipError_t launch_swiglu(const SwigluArgs& a, hipStream_t s) {
-    using T = SwigluTile;
+template <class T>
+static hipError_t launch_swiglu_tiles(const SwigluArgs& a, hipStream_t s) {
     static_assert(kHidden % (6 * T::BK) == 0, "the K loop walks its stages six at a time");
     const int grid = gemm::tile_grid_split<gemm::kSwigluSlices>((a.rows + T::BM - 1) / T::BM, 2 * kFF / T::BN);
     if (a.stats) hipLaunchKernelGGL((gemm::swiglu_kernel<T, true>), dim3(grid), dim3(T::THREADS), 0, s, a);
     else hipLaunchKernelGGL((gemm::swiglu_kernel<T, false>), dim3(grid), dim3(T::THREADS), 0, s, a);
     return hipGetLastError();
+}
+
+hipError_t launch_swiglu(const SwigluArgs& a, hipStream_t s) {
+    return a.rows < kSwigluSmallRows ? launch_swiglu_tiles<SwigluTileS>(a, s) : launch_swiglu_tiles<SwigluTile>(a, s);
 }
 
 hipError_t launch_splitk(const SplitKArgs& a, hipStream_t s) {
