@@ -369,9 +369,9 @@ __global__ __launch_bounds__(T::THREADS, T::BK == 128 ? 3 : 4) void resid_kernel
 // the constants wait in LDS. The epilogue turns each 16-column half of a
 // 32-column act block into a fragment in registers (frag_swap) and writes
 // it whole (act is in fragment order).
-constexpr int kSwigluSlices = 2;  // N slices of the XCD tile split (xcd_tile_split)
-
-template <class T, bool LN>
+// NS: N slices of the XCD tile split (xcd_tile_split); the launcher picks
+// it by the launch's size.
+template <class T, bool LN, int NS>
 __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void swiglu_kernel(SwigluArgs p) {
     static_assert(T::TN % 64 == 0 && T::WGN == 1, "whole gate/up pairs, whole rows per wave");
     static_assert(T::BN <= T::THREADS, "one thread per column constant");
@@ -386,7 +386,7 @@ __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void swiglu_kernel(
     float4_t raw[T::FM][3];
     RowNorm rn[T::FM];
     float cb = 0.f, cw = 0.f;
-    gemm_tile_dma<T, kSwigluSlices, kHidden / T::BK>(
+    gemm_tile_dma<T, NS, kHidden / T::BK>(
         al, wd, wb0, wb1, wb2, NT, NT * ((p.rows + T::BM - 1) / T::BM), kHidden / T::BK,
         [&](int m0, int n0) {
             const Frag<T> f(m0, n0);

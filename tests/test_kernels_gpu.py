@@ -336,7 +336,7 @@ def pack_gateup(wg, wu, bg, bu):
     return w, b
 
 
-@pytest.mark.parametrize("rows", [1, 33, 257, 1001, 12864])
+@pytest.mark.parametrize("rows", [1, 33, 257, 1001, 6432, 12864])
 def test_swiglu(eng, rows):
     rng = np.random.default_rng(rows)
     h = f16(rng.normal(size=(rows, 384)))
