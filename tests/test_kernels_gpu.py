@@ -503,7 +503,7 @@ def test_qkv_rope_layernorm_fused(eng, images, grid, offset):
         check(gv[i, :, :T].transpose(1, 0, 2).reshape(T, 384), rv, atol=3e-3, what=f"fused-LN v img {i}")
 
 
-@pytest.mark.parametrize("rows,offset", [(33, 1.0), (1001, 0.0), (12864, 2.0)])
+@pytest.mark.parametrize("rows,offset", [(33, 1.0), (1001, 0.0), (6432, 1.0), (12864, 2.0)])
 def test_swiglu_layernorm_fused(eng, rows, offset):
     rng = np.random.default_rng(rows + 17)
     x = f16(rng.normal(size=(rows, 384)) + offset)
