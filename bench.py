@@ -171,6 +171,7 @@ def ceilings(d, full=False):
     if full:
         out["valu_fma_per_mfma"] = {n: d.probe("valu", n) for n in (0, 2, 4, 6, 8)}
         out["exp2_per_mfma"] = {n: d.probe("exp2", n) for n in (1, 2)}
+        out["accumulator_chains"] = {n: d.probe("chains", n) for n in (1, 2, 4, 8)}
         for where in ("l1", "l2", "hbm"):
             rows = {n: d.probe(f"loads_{where}", n) for n in (0, 2, 3, 4, 6)}
             for n, r in rows.items():  # per-CU load rate: 4 waves x n KB per 8-MFMA iteration

@@ -82,6 +82,31 @@ mfma_valu_kernel(const half8_t* src, float* sink, int iters, ProbeOut* out) {
     if (threadIdx.x == 0) out[blockIdx.x].cycles = t1 - t0;
 }
 
+// 8 MFMAs per iteration on CHAINS independent accumulators (MFMA j adds into
+// accumulator j % CHAINS): with fewer chains each MFMA depends on the one
+// CHAINS positions before it, as in a GEMM wave tile of CHAINS 32x32 blocks
+// (the residual GEMMs' 32 x 64 wave tiles are two chains).
+template <int CHAINS>
+__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads), amdgpu_waves_per_eu(1, 1))) void
+mfma_chain_kernel(const half8_t* src, float* sink, int iters, ProbeOut* out) {
+    half8_t a[4], b[2];
+    load_operands(src, a, b);
+    float16_t acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = float16_t{};
+    const long long t0 = __builtin_amdgcn_s_memtime();
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            acc[j % CHAINS] = mfma32x32x16(a[j % 4], b[j / 4], acc[j % CHAINS]);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        }
+    }
+    const long long t1 = __builtin_amdgcn_s_memtime();
+    sink[(size_t)blockIdx.x * kThreads + threadIdx.x] = reduce_acc(acc);
+    if (threadIdx.x == 0) out[blockIdx.x].cycles = t1 - t0;
+}
+
 // LOADS 16-byte buffer loads per 8 MFMAs, each lane 16 B per load, the wave
 // cycling through FOOT KB of its own (a compile-time power of two, so the
 // block index costs one mask); the loaded fragments feed the MFMAs three
@@ -143,22 +168,25 @@ extern "C" int dhx_probe(int32_t device, int32_t kind, int32_t param, double* re
     // [2] clock implied (GHz) = cycles / elapsed time. Kinds: 0 MFMAs on
     // random operands, 1 on zeros, 2 with param VALU FMAs per MFMA, 3 with
     // param exp2 per MFMA, 4/5/6 with param buffer loads per 8 MFMAs from an
-    // 8 KB (L1) / 16 KB (L2) / 512 KB (HBM) footprint per wave.
+    // 8 KB (L1) / 16 KB (L2) / 512 KB (HBM) footprint per wave, 7 on param
+    // independent accumulator chains.
     if (!results) return 1;
     static const int kValu[] = {0, 2, 4, 6, 8};
     static const int kTrans[] = {1, 2};
     static const int kLoads[] = {0, 2, 3, 4, 6};
     static const int kFoot[] = {8, 16, 512};  // KB per wave: L1, L2, HBM
+    static const int kChains[] = {1, 2, 4, 8};
     auto in = [](int v, const int* set, int n) {
         for (int i = 0; i < n; ++i)
             if (set[i] == v) return true;
         return false;
     };
-    if (kind < 0 || kind > 6) return 2;
+    if (kind < 0 || kind > 7) return 2;
     if ((kind == 1 || kind == 0) && param != 0) return 2;
     if (kind == 2 && !in(param, kValu, 5)) return 2;
     if (kind == 3 && !in(param, kTrans, 2)) return 2;
-    if (kind >= 4 && !in(param, kLoads, 5)) return 2;
+    if (kind >= 4 && kind <= 6 && !in(param, kLoads, 5)) return 2;
+    if (kind == 7 && !in(param, kChains, 4)) return 2;
     PROBE_CHECK(hipSetDevice(device));
     const size_t lanes = (size_t)kBlocks * kThreads;
     std::vector<half_t> host(lanes * kOperands * 8);
@@ -167,12 +195,12 @@ extern "C" int dhx_probe(int32_t device, int32_t kind, int32_t param, double* re
         x = x * 1664525u + 1013904223u;
         h = kind == 1 ? (half_t)0.f : (half_t)(((x >> 8) / 16777216.f - 0.5f) * 4.f);
     }
-    const int foot = kind >= 4 ? kFoot[kind - 4] : 0;  // 4: L1 (8 KB), 5: L2 (16 KB), 6: HBM (512 KB)
+    const int foot = kind >= 4 && kind <= 6 ? kFoot[kind - 4] : 0;  // 4: L1 (8 KB), 5: L2 (16 KB), 6: HBM (512 KB)
     half8_t* src = nullptr;
     half_t* pool = nullptr;
     float* sink = nullptr;
     ProbeOut* out = nullptr;
-    const uint64_t pool_bytes = kind >= 4 ? (uint64_t)kBlocks * 4 * foot * 1024 : 0;
+    const uint64_t pool_bytes = (uint64_t)kBlocks * 4 * foot * 1024;
     hipEvent_t e0 = nullptr, e1 = nullptr;
     int rc = 1;
     do {
@@ -207,6 +235,14 @@ extern "C" int dhx_probe(int32_t device, int32_t kind, int32_t param, double* re
             case 3:
                 if (param == 1) hipLaunchKernelGGL((mfma_valu_kernel<1, true>), g, t, 0, 0, src, sink, iters, out);
                 else hipLaunchKernelGGL((mfma_valu_kernel<2, true>), g, t, 0, 0, src, sink, iters, out);
+                break;
+            case 7:
+                switch (param) {
+                case 1: hipLaunchKernelGGL((mfma_chain_kernel<1>), g, t, 0, 0, src, sink, iters, out); break;
+                case 2: hipLaunchKernelGGL((mfma_chain_kernel<2>), g, t, 0, 0, src, sink, iters, out); break;
+                case 4: hipLaunchKernelGGL((mfma_chain_kernel<4>), g, t, 0, 0, src, sink, iters, out); break;
+                default: hipLaunchKernelGGL((mfma_chain_kernel<8>), g, t, 0, 0, src, sink, iters, out); break;
+                }
                 break;
             default: {
                 const uint64_t pb = pool_bytes;

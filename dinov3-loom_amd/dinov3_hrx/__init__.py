@@ -335,14 +335,15 @@ def patchify(pixels, image_size: int = 224) -> np.ndarray:
 
 
 PROBE_KINDS = {"mfma_random": 0, "mfma_zeros": 1, "valu": 2, "exp2": 3, "loads_l1": 4, "loads_l2": 5,
-               "loads_hbm": 6}
+               "loads_hbm": 6, "chains": 7}
 
 
 def probe(kind: str, param: int = 0, device: int = 0) -> dict:
     """Machine-ceiling probe (dhx_probe): one wave per SIMD running 32x32x16
     f16 MFMAs alone or beside `param` VALU FMAs / exp2 per MFMA or `param`
-    buffer loads per 8 MFMAs. Returns cycles per 8 MFMAs of a wave, TFLOP/s
-    over the GPU and the clock they imply (GHz)."""
+    buffer loads per 8 MFMAs, or ("chains") on `param` independent
+    accumulators. Returns cycles per 8 MFMAs of a wave, TFLOP/s over the GPU
+    and the clock they imply (GHz)."""
     out = (ctypes.c_double * 3)()
     rc = _lib.dhx_probe(int(device), PROBE_KINDS[kind], int(param), out)
     if rc == 2:

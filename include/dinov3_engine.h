@@ -210,8 +210,10 @@ int dhx_launch_timings(dhx_engine *e, uint64_t batch, uint32_t iters, double *ms
  * random operands (param 0), 1 on zeros (param 0), 2 with param VALU FMAs per
  * MFMA (0, 2, 4, 6, 8), 3 with param exp2 per MFMA (1, 2), 4 / 5 / 6 with param
  * 16-byte buffer loads per 8 MFMAs (0, 2, 3, 4, 6) from an 8 KB (L1) / 16 KB
- * (L2) / 512 KB (HBM) footprint per wave. Returns 0, 2 for an unsupported
- * (kind, param), 1 on a HIP error. Allocates its own buffers. */
+ * (L2) / 512 KB (HBM) footprint per wave, 7 with the MFMAs on param (1, 2, 4,
+ * 8) independent accumulators (MFMA j adds into accumulator j % param).
+ * Returns 0, 2 for an unsupported (kind, param), 1 on a HIP error. Allocates
+ * its own buffers. */
 int dhx_probe(int32_t device, int32_t kind, int32_t param, double *results);
 
 /* No reference counterpart (test hook): make the next HIP-facing engine call

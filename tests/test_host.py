@@ -54,7 +54,7 @@ def test_binding_structs_match_header(tmp_path):
 
 def test_probe_rejects_unsupported_arguments():
     # Checked before any HIP call, so this runs without a GPU.
-    for kind, param in (("valu", 3), ("exp2", 0), ("loads_l2", 5), ("mfma_random", 1)):
+    for kind, param in (("valu", 3), ("exp2", 0), ("loads_l2", 5), ("mfma_random", 1), ("chains", 3), ("chains", 0)):
         with pytest.raises(d.DINOv3Error, match="unsupported probe"):
             d.probe(kind, param)
 

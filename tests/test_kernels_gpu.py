@@ -777,3 +777,8 @@ def test_machine_ceiling_probes():
     assert r["tflops"] > 0.5 * 2500 * r["clock_ghz"] / 2.4, r
     l1 = d.probe("loads_l1", 2)
     assert l1["cycles_per_8_mfma"] <= 1.1 * r["cycles_per_8_mfma"], l1
+    # Eight independent accumulators issue at the full rate; one chain of
+    # dependent MFMAs can be no faster.
+    c8, c1 = d.probe("chains", 8), d.probe("chains", 1)
+    assert 250 <= c8["cycles_per_8_mfma"] <= 270, c8
+    assert c1["cycles_per_8_mfma"] >= c8["cycles_per_8_mfma"] - 1, c1
