@@ -116,7 +116,9 @@ def replay_distribution(model, b, samples):
 def sync_stats(model, b, samples):
     med, p95 = replay_distribution(model, b, samples)
     return {"median_ms": round(med * 1e3, 4), "p95_ms": round(p95 * 1e3, 4), "samples": samples,
-            "images_per_s_at_median": round(b / med, 1)}
+            "images_per_s_at_median": round(b / med, 1),
+            "what": "the reference's ForwardTimings statistic (engine.rs:130-190): host clock around each replay "
+                    "with a synchronisation before and after; median t[n/2] and p95 t[ceil(0.95 n) - 1]"}
 
 
 def read_sclk_mhz():
@@ -163,17 +165,19 @@ def sustained(model, b, seconds=4.0, chunk=40):
                     "samples dropped while it settles)"}
 
 
-def ceilings(d, full=False):
-    """Machine ceilings from dhx_probe (one wave per SIMD, 32x32x16 f16 MFMAs):
-    the MFMA loop alone on random and on zero operands, and with full=True the
-    vector work and the load rates that still leave the MFMAs unslowed."""
-    out = {"mfma_random": d.probe("mfma_random"), "mfma_zeros": d.probe("mfma_zeros")}
+def ceilings(full=False):
+    """Machine ceilings from dhx_probe (one wave per SIMD, 32x32x16 f16 MFMAs;
+    the measurement library libdinov3_probe.so, not the forward's): the MFMA
+    loop alone on random and on zero operands, and with full=True the vector
+    work and the load rates that still leave the MFMAs unslowed."""
+    from dinov3_hrx.ceilings import probe
+    out = {"mfma_random": probe("mfma_random"), "mfma_zeros": probe("mfma_zeros")}
     if full:
-        out["valu_fma_per_mfma"] = {n: d.probe("valu", n) for n in (0, 2, 4, 6, 8)}
-        out["exp2_per_mfma"] = {n: d.probe("exp2", n) for n in (1, 2)}
-        out["accumulator_chains"] = {n: d.probe("chains", n) for n in (1, 2, 4, 8)}
+        out["valu_fma_per_mfma"] = {n: probe("valu", n) for n in (0, 2, 4, 6, 8)}
+        out["exp2_per_mfma"] = {n: probe("exp2", n) for n in (1, 2)}
+        out["accumulator_chains"] = {n: probe("chains", n) for n in (1, 2, 4, 8)}
         for where in ("l1", "l2", "hbm"):
-            rows = {n: d.probe(f"loads_{where}", n) for n in (0, 2, 3, 4, 6)}
+            rows = {n: probe(f"loads_{where}", n) for n in (0, 2, 3, 4, 6)}
             for n, r in rows.items():  # per-CU load rate: 4 waves x n KB per 8-MFMA iteration
                 r["cu_bytes_per_clk"] = round(4 * n * 1024 / r["cycles_per_8_mfma"], 1)
             out[f"loads_{where}_per_8_mfma"] = rows
@@ -216,13 +220,15 @@ def cpu_baseline(path, seconds):
         return n, time.perf_counter() - t0
 
     n, dt = run(1, seconds)
-    cores = min(16, len(os.sched_getaffinity(0)))
+    usable = len(os.sched_getaffinity(0))
+    cores = min(16, usable)
     nm, dtm = run(cores, seconds / 3)
     return {"value": round(n / dt, 4), "unit": "images/s", "cores": 1, "kind": "port", "cpu": cpu_model(),
             "sample": f"{n} image(s) of the b=64 workload at 224x224 through the float64 C oracle "
                       f"(oracle/dinov3_oracle.c), 1 thread, {dt:.1f} s",
-            "all_cores": {"value": round(nm / dtm, 4), "cores": cores,
-                          "sample": f"{nm} image(s), {cores} threads, {dtm:.1f} s"}}
+            "all_cores": {"value": round(nm / dtm, 4), "cores": cores, "nproc": os.cpu_count(),
+                          "usable_cpus": usable,
+                          "sample": f"{nm} image(s), {cores} threads (min(16, usable CPUs)), {dtm:.1f} s"}}
 
 
 def library_gemms(batch, iters=20, reps=30):
@@ -274,6 +280,11 @@ def main():
                     help="skip the batch-32, batch-1, end-to-end and 512x512 measurements (for profiling runs)")
     ap.add_argument("--branches", type=int, default=0,
                     help="image groups run as concurrent graph branches (0: pick 1-4 by a short trial)")
+    ap.add_argument("--down-proj", choices=("auto", "resid", "splitk"), default="auto",
+                    help="down-projection variant (auto: pick by a short trial)")
+    ap.add_argument("--unfused-layernorm", action="store_true",
+                    help="run the plan with separate f16 LayerNorm kernels (the reference's) instead of LayerNorm "
+                         "folded into the QKV and gate/up GEMMs (for profiling those kernels)")
     ap.add_argument("--library-gemms", action="store_true",
                     help="only time the vendor library's GEMMs at the forward's shapes (a reference table)")
     ap.add_argument("--ceilings", action="store_true",
@@ -284,8 +295,7 @@ def main():
         library_gemms(args.batch)
         return
     if args.ceilings:
-        import dinov3_hrx as d
-        print(json.dumps(ceilings(d, full=True)))
+        print(json.dumps(ceilings(full=True)))
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the forward would shard by image, "
@@ -303,13 +313,15 @@ def main():
         d.write_random_weights(path, seed=0, preset=0)
         model = d.DINOv3.load(path, d.Options(device=0, max_batch=max(b, 32) if full else b, image_size=S))
         px = d.random_pixels(1, b, S)
+        if args.unfused_layernorm:
+            model.set_layernorm_fusion(0)
 
         # Pick the down-projection variant (the reference uses the residual
         # GEMM for b > 1, split-K at b = 1) and the number of image groups run
         # side by side by a short trial: every grouping gives the same bits,
         # the two variants agree to f16 rounding.
         trial = {}
-        for mode in (0, 1):
+        for mode in {"auto": (0, 1), "resid": (0,), "splitk": (1,)}[args.down_proj]:
             for nb in ([args.branches] if args.branches else range(1, max(1, min(4, b // 4)) + 1)):
                 model.set_splitk(mode)
                 model.set_branches(nb)
@@ -345,7 +357,7 @@ def main():
             roof = {"kernel": dom["kernel"], "bound": "hbm", "achieved": dom["gbs"], "peak": PEAK_GBS,
                     "unit": "GB/s", "frac": round(dom["gbs"] / PEAK_GBS, 4)}
         roof["traffic"] = measured_traffic(dom["kernel"]) if (b == 64 and S == 224) else None
-        ceiling = ceilings(d) if full else None
+        ceiling = ceilings() if full else None
         if ceiling:
             # The MFMA loop alone on random operands, on this GPU and its power
             # budget: what the published peak shrinks to once the clock drops.
@@ -389,8 +401,12 @@ def main():
         "config": {"workload": f"DINOv3 ViT-S+/16 forward, {S}x{S}, batch {b}, resident hipGraph replay "
                                f"(BASELINE.json config {3 if S == 224 else 5})", "batch": b, "image_size": S, "tokens": T,
                    "down_proj": "splitk" if mode == 1 else "resid", "branches": branches,
+                   "layernorm": "separate kernels" if args.unfused_layernorm else "folded into the GEMMs",
                    "weights": "seeded random init (BASELINE)"},
         "mfma_frac_forward": round(value * gflop_image / 1e3 / PEAK_TFLOPS, 4),
+        "value_scope": f"back-to-back replays: batch / (host time of {args.steps} replays queued without waiting, "
+                       f"one synchronisation before and after / {args.steps}), after {args.warmup} warmup replays; "
+                       "sync_replay is the reference's per-replay statistic",
         "sync_replay": sync,
     }
     if full:

@@ -1,7 +1,10 @@
-"""Build recipe for libdinov3_hrx.so: every HIP kernel and host source is
-compiled with hipcc for gfx950 (wave64) and linked into one shared library
-that exports the C ABI of include/dinov3.h and include/dinov3_engine.h; the
-command-line front end lib/dinov3-hrx (csrc/cli.cpp) links against it.
+"""Build recipe for libdinov3_hrx.so: every HIP kernel and host source of the
+forward pass is compiled with hipcc for gfx950 (wave64) and linked into one
+shared library that exports the C ABI of include/dinov3.h and
+include/dinov3_engine.h; the command-line front end lib/dinov3-hrx
+(csrc/cli.cpp) links against it. The machine-ceiling probes
+(csrc/kernels/probe.hip, include/dinov3_probe.h) go into a library of their
+own, lib/libdinov3_probe.so, which only bench.py and the tests load.
 
     python dinov3-loom_amd/build.py [-j N]
 """
@@ -18,13 +21,14 @@ CSRC = os.path.join(HERE, "csrc")
 LIB_DIR = os.path.join(HERE, "lib")
 OBJ_DIR = os.path.join(LIB_DIR, "obj")
 LIB_PATH = os.path.join(LIB_DIR, "libdinov3_hrx.so")
+PROBE_LIB_PATH = os.path.join(LIB_DIR, "libdinov3_probe.so")
 CLI_PATH = os.path.join(LIB_DIR, "dinov3-hrx")
 
+PROBE_SOURCES = ["kernels/probe.hip"]
 SOURCES = [
     "kernels/gemm.hip",
     "kernels/attention.hip",
     "kernels/norm.hip",
-    "kernels/probe.hip",
     "engine.cpp",
     "model.cpp",
     "weights.cpp",
@@ -50,7 +54,7 @@ def _compile_cmd(src: str) -> tuple[list[str], str]:
 
 def build(jobs: int = 8, verbose: bool = False) -> str:
     os.makedirs(OBJ_DIR, exist_ok=True)
-    cmds = [_compile_cmd(s) for s in SOURCES]
+    cmds = [_compile_cmd(s) for s in SOURCES + PROBE_SOURCES]
     running: list[tuple[subprocess.Popen, list[str]]] = []
     failed = []
 
@@ -78,10 +82,11 @@ def build(jobs: int = 8, verbose: bool = False) -> str:
     if failed:
         msg = "\n\n".join(" ".join(c) + "\n" + t for c, t in failed)
         raise RuntimeError(f"hipcc failed:\n{msg}")
-    tmp = LIB_PATH + ".tmp"
-    link = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *[o for _, o in cmds], "-o", tmp]
-    subprocess.check_call(link)
-    os.replace(tmp, LIB_PATH)
+    probe_objs = [o for _, o in cmds[len(SOURCES):]]
+    for path, objs in ((LIB_PATH, [o for _, o in cmds[:len(SOURCES)]]), (PROBE_LIB_PATH, probe_objs)):
+        tmp = path + ".tmp"
+        subprocess.check_call([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp])
+        os.replace(tmp, path)
     build_cli()
     return LIB_PATH
 

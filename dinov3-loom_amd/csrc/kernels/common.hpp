@@ -28,6 +28,15 @@ constexpr float kLn2 = 0.6931471805599453f;
 // index stride.
 constexpr int kBufferRsrcWord3 = 0x00020000;
 
+// A 64-bit address from its two 32-bit words as __builtin_amdgcn_readfirstlane
+// returns them (int). Each word is widened through uint32_t: widened as a
+// signed int, a low word with bit 31 set would sign-extend and overwrite the
+// high word with ones (0x80000000 -> 0xffffffff80000000), and stores through
+// such a base fault.
+__host__ __device__ constexpr uint64_t address_from_words(int lo, int hi) {
+    return ((uint64_t)(uint32_t)hi << 32) | (uint64_t)(uint32_t)lo;
+}
+
 // Output stores that write through the L2: 16-byte buffer stores with the
 // sc1 cache policy. On this multi-XCD GPU every dispatch ends by writing its
 // dirty L2 lines back (the XCDs' L2s are not coherent with each other), and
@@ -41,13 +50,11 @@ constexpr int kBufferRsrcWord3 = 0x00020000;
 struct WtOut {
     __amdgpu_buffer_rsrc_t r;
     __device__ __forceinline__ WtOut(const void* base, uint32_t bytes) {
-        // readfirstlane returns int: each word goes back through uint32_t, or
-        // a low word with bit 31 set would sign-extend over the high word.
         const uint64_t a = (uint64_t)(uintptr_t)base;
-        const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a);
-        const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
-        r = __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)((hi << 32) | lo), 0,
-                                              (int)__builtin_amdgcn_readfirstlane(bytes), kBufferRsrcWord3);
+        const uint64_t u = address_from_words(__builtin_amdgcn_readfirstlane((uint32_t)a),
+                                              __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)));
+        r = __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)u, 0, (int)__builtin_amdgcn_readfirstlane(bytes),
+                                              kBufferRsrcWord3);
     }
     template <class V>
     __device__ __forceinline__ void store(uint32_t byte_off, V v) const {

@@ -22,6 +22,12 @@ using SwigluTile = Tile<256, 128, 4, 1, 64>;
 // batches): 128-row tiles, three workgroups per CU instead of two.
 using SwigluTileS = Tile<128, 128, 4, 1, 64>;
 constexpr int kSwigluSmallRows = 4096;
+// The folded LayerNorm's -mean * wsum term joins column block i's
+// accumulators at K step i + 1, so where it enters the fp32 sum depends on
+// the stage depth. Both tile shapes must share it for a row's result to be
+// bitwise the same whichever shape its launch takes (the image groupings of
+// the forward and the allocation-free entry point rely on that).
+static_assert(SwigluTile::BK == SwigluTileS::BK, "one stage depth for every SwiGLU tile shape");
 using SplitTile = Tile<128, 128, 4, 1>;
 
 template <class T, class Args>

@@ -1,4 +1,5 @@
-// Machine-ceiling probes for the roofline (dhx_probe in dinov3_engine.h): what
+// Machine-ceiling probes for the roofline (dhx_probe in dinov3_probe.h, built
+// into the measurement library libdinov3_probe.so, not the forward's): what
 // one CU of this GPU sustains while 32x32x16 f16 MFMAs run, measured with the
 // wave's own cycle counter (s_memtime). Every probe runs one workgroup of four
 // waves per CU (one wave per SIMD, the whole register file each) on 256
@@ -20,6 +21,7 @@
 #include <vector>
 
 #include "common.hpp"
+#include "dinov3_probe.h"
 
 namespace dhx {
 namespace {

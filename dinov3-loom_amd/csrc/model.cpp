@@ -86,21 +86,59 @@ constexpr uint64_t kScratchBytes = DINOV3_NOALLOC_SCRATCH_BYTES;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 constexpr int kMaxDevices = 64;
-std::mutex g_scratch_mutex;
-void* g_scratch[kMaxDevices] = {};
 
-void* scratch_address(int device) {
-    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+// Restores the calling thread's current device when it goes out of scope.
+class DeviceGuard {
+public:
+    DeviceGuard() {
+        if (hipGetDevice(&prev_) != hipSuccess) prev_ = -1;
+    }
+    ~DeviceGuard() {
+        if (prev_ >= 0) (void)hipSetDevice(prev_);
+    }
+    DeviceGuard(const DeviceGuard&) = delete;
+    DeviceGuard& operator=(const DeviceGuard&) = delete;
+
+private:
+    int prev_ = -1;
+};
+
+// Per device: the array's address on that device, and an event recorded
+// after the launches of the last allocation-free call queued there. Each
+// call's stream waits for that event before its first launch, so calls on
+// one GPU run one after another whatever their streams, threads or models.
+// Both are created once (the first model load on the device) and kept
+// until the process ends, like the array.
+struct ScratchSlot {
+    void* ptr = nullptr;
+    hipEvent_t last = nullptr;
+};
+std::mutex g_scratch_mutex;  // guards g_scratch and orders the queueing of calls
+ScratchSlot g_scratch[kMaxDevices];
+
+// Callers hold g_scratch_mutex. Leaves the caller's current device as it was.
+ScratchSlot& scratch_slot_locked(int device) {
     if (device < 0 || device >= kMaxDevices) throw Error("device id out of range for the scratch table");
-    if (!g_scratch[device]) {
+    ScratchSlot& s = g_scratch[device];
+    if (!s.ptr) {
+        DeviceGuard keep;
         hipError_t err = hipSetDevice(device);
         void* p = nullptr;
         if (err == hipSuccess) err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (err != hipSuccess || !p)
             throw Error(std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(err));
-        g_scratch[device] = p;
+        hipEvent_t ev = nullptr;
+        err = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+        if (err != hipSuccess) throw Error(std::string("hipEventCreateWithFlags: ") + hipGetErrorString(err));
+        s.ptr = p;
+        s.last = ev;
     }
-    return g_scratch[device];
+    return s;
+}
+
+void* scratch_address(int device) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    return scratch_slot_locked(device).ptr;
 }
 
 constexpr uint64_t align256(uint64_t v) { return (v + 255) & ~255ull; }
@@ -403,6 +441,17 @@ public:
         if (at > kScratchBytes)
             throw Error("the allocation-free forward of " + std::to_string(images) + " images needs " +
                         std::to_string(at) + " bytes of scratch, more than its " + std::to_string(kScratchBytes));
+        // One call at a time binds, plans and queues its launches on this
+        // GPU (the lock also keeps two threads of one model from rebinding
+        // each other's input and output), and each call's stream waits for
+        // the previous call's launches (its event), so overlapping calls
+        // from other streams, threads or models run in turn instead of
+        // racing on the array. Under stream capture the wait and the record
+        // are left out (the graph's launches are ordered by whoever launches
+        // the graph), and nothing else changes.
+        DeviceGuard keep;
+        std::lock_guard<std::mutex> lock(g_scratch_mutex);
+        ScratchSlot& slot = scratch_slot_locked(dhx::engine_device(e));
         const uint64_t in_bytes = images * image_elems_ * 4, out_bytes = r * kHiddenU * 4;
         dhx::engine_rebind(e, ext_in_, const_cast<float*>(pixels), in_bytes);
         dhx::engine_rebind(e, ext_out_, out, out_bytes);
@@ -410,15 +459,20 @@ public:
         bufs[kOut] = bufs[kOut1] = dhx_region{ext_out_, 0, out_bytes};
         noalloc_launches_.clear();  // capacity reserved at load: no reallocation
         plan(0, images, images, 0, 0, noalloc_launches_, bufs);
-        char* const base = static_cast<char*>(scratch_address(dhx::engine_device(e)));
+        char* const base = static_cast<char*>(slot.ptr);
         const dhx::PadRowsArgs pad{reinterpret_cast<dhx::half_t*>(base + bufs[kQ].offset),
                                    reinterpret_cast<dhx::half_t*>(base + bufs[kK].offset),
                                    reinterpret_cast<dhx::half_t*>(base + bufs[kV].offset), (int)images, (int)tokens_,
                                    (int)tpad_};
         if (!stream) stream = dhx::engine_stream(e);
         dhx::engine_check(e, hipSetDevice(dhx::engine_device(e)), "hipSetDevice");
+        hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+        dhx::engine_check(e, hipStreamIsCapturing(stream, &capture), "hipStreamIsCapturing");
+        const bool ordered = capture == hipStreamCaptureStatusNone;
+        if (ordered) dhx::engine_check(e, hipStreamWaitEvent(stream, slot.last, 0), "hipStreamWaitEvent");
         dhx::engine_check(e, dhx::launch_zero_pad_rows(pad, stream), "kernel launch");
         dhx::engine_queue(e, noalloc_launches_.data(), noalloc_launches_.size(), stream);
+        if (ordered) dhx::engine_check(e, hipEventRecord(slot.last, stream), "hipEventRecord");
     }
 
     // Number of image groups run side by side for a batch of b.

@@ -109,7 +109,6 @@ def _load_library() -> ctypes.CDLL:
                                      c.c_uint64, c.POINTER(c.c_uint64)]
     L.dhx_has_graph.argtypes = [vp, c.c_uint64]
     L.dhx_test_fail_next_call.argtypes = [vp]
-    L.dhx_probe.argtypes = [c.c_int32, c.c_int32, c.c_int32, c.POINTER(c.c_double)]
     L.dhx_engine_open.argtypes = [c.c_int32, c.POINTER(vp)]
     L.dhx_engine_free.argtypes = [vp]
     L.dhx_allocate.argtypes = [vp, c.c_uint64, c.POINTER(Region)]
@@ -332,25 +331,6 @@ def patchify(pixels, image_size: int = 224) -> np.ndarray:
     out = np.empty((images * g * g, 768), np.float32)
     _check(_lib.dinov3_patchify(_fptr(px), images, int(image_size), _fptr(out)))
     return out
-
-
-PROBE_KINDS = {"mfma_random": 0, "mfma_zeros": 1, "valu": 2, "exp2": 3, "loads_l1": 4, "loads_l2": 5,
-               "loads_hbm": 6, "chains": 7}
-
-
-def probe(kind: str, param: int = 0, device: int = 0) -> dict:
-    """Machine-ceiling probe (dhx_probe): one wave per SIMD running 32x32x16
-    f16 MFMAs alone or beside `param` VALU FMAs / exp2 per MFMA or `param`
-    buffer loads per 8 MFMAs, or ("chains") on `param` independent
-    accumulators. Returns cycles per 8 MFMAs of a wave, TFLOP/s over the GPU
-    and the clock they imply (GHz)."""
-    out = (ctypes.c_double * 3)()
-    rc = _lib.dhx_probe(int(device), PROBE_KINDS[kind], int(param), out)
-    if rc == 2:
-        raise DINOv3Error(f"unsupported probe {kind} with param {param}")
-    if rc != 0:
-        raise DINOv3Error(f"probe {kind} failed (HIP error)")
-    return {"cycles_per_8_mfma": out[0], "tflops": out[1], "clock_ghz": out[2]}
 
 
 def fragment_order(a: np.ndarray) -> np.ndarray:

@@ -90,8 +90,13 @@ int dinov3_benchmark(dinov3_model *m, const float *pixels, uint64_t n_floats, ui
  * that the pixels are finite. A batch whose buffers do not fit the array (beyond about 43 images
  * at 224x224, 9 at 512x512) fails with an error naming the sizes, before
  * anything is queued. Every call on one GPU uses that GPU's single array and
- * leaves its data there: calls that overlap in time on one GPU (other
- * streams, threads or models) race and give wrong results. */
+ * leaves its data there, so calls on one GPU are run one after another:
+ * each call's stream waits (hipStreamWaitEvent, no host wait) for the
+ * launches of the call queued before it on that GPU, from any stream,
+ * thread or model. A call made while `stream` is being captured into a HIP
+ * graph is queued without that wait: replays of the graph use the same
+ * array, and the caller must not let them overlap other calls on that GPU.
+ * The caller's current device is left as it was. */
 #define DINOV3_NOALLOC_SCRATCH_BYTES (64ull << 20)
 int dinov3_forward_noalloc(dinov3_model *m, const float *pixels, uint64_t images, float *out, void *stream);
 const char *dinov3_last_error(const dinov3_model *m);

@@ -202,20 +202,6 @@ int dhx_copy_out_finish(dhx_engine *e, void *dst, uint64_t n, uint32_t slot);
 int dhx_launch_timings(dhx_engine *e, uint64_t batch, uint32_t iters, double *ms_out,
                        uint32_t *kernel_out, uint64_t capacity, uint64_t *count);
 
-/* No reference counterpart (measurement hook for the roofline): machine-ceiling
- * probes on `device`, one workgroup of four waves per CU (one wave per SIMD),
- * 256 workgroups, 32x32x16 f16 MFMAs on 8 independent accumulators.
- * results[0] = s_memtime cycles per 8 MFMAs of one wave, results[1] = TFLOP/s
- * over the GPU, results[2] = the clock those two imply (GHz). kind: 0 MFMAs on
- * random operands (param 0), 1 on zeros (param 0), 2 with param VALU FMAs per
- * MFMA (0, 2, 4, 6, 8), 3 with param exp2 per MFMA (1, 2), 4 / 5 / 6 with param
- * 16-byte buffer loads per 8 MFMAs (0, 2, 3, 4, 6) from an 8 KB (L1) / 16 KB
- * (L2) / 512 KB (HBM) footprint per wave, 7 with the MFMAs on param (1, 2, 4,
- * 8) independent accumulators (MFMA j adds into accumulator j % param).
- * Returns 0, 2 for an unsupported (kind, param), 1 on a HIP error. Allocates
- * its own buffers. */
-int dhx_probe(int32_t device, int32_t kind, int32_t param, double *results);
-
 /* No reference counterpart (test hook): make the next HIP-facing engine call
  * fail as if the runtime had returned an error, to exercise poisoning. */
 int dhx_test_fail_next_call(dhx_engine *e);

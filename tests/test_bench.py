@@ -87,6 +87,9 @@ def test_bench_json_line(gpu):
     assert abs(roof["achieved"] - work / (roof["avg_us"] * 1e-6)) <= 0.01 * roof["achieved"]
     cpu = d["cpu_baseline"]
     assert cpu["kind"] == "port" and cpu["cores"] == 1 and cpu["value"] > 0 and cpu["sample"]
+    assert cpu["all_cores"]["nproc"] >= cpu["all_cores"]["usable_cpus"] >= cpu["all_cores"]["cores"] >= 1
+    # what `value` and `sync_replay` each time
+    assert "back-to-back" in d["value_scope"] and "engine.rs:130-190" in d["sync_replay"]["what"]
 
 
 def test_sync_replay_statistics(monkeypatch):

@@ -11,14 +11,15 @@ import numpy as np
 import pytest
 
 import dinov3_hrx as d
+from dinov3_hrx import ceilings
 import oracle
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def declared_functions():
+def declared_functions(headers=("dinov3.h", "dinov3_engine.h")):
     names = []
-    for h in ("dinov3.h", "dinov3_engine.h"):
+    for h in headers:
         text = open(os.path.join(ROOT, "include", h)).read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
         names += re.findall(r"\b((?:dinov3|dhx)_[a-z0-9_]+)\s*\(", text)
@@ -31,6 +32,12 @@ def test_library_exports_every_declared_function():
     assert len(names) > 30
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
+    # The machine-ceiling probes live in their own measurement library.
+    probe_names = declared_functions(("dinov3_probe.h",))
+    assert probe_names == ["dhx_probe"]
+    assert not hasattr(lib, "dhx_probe")
+    probe_lib = ctypes.CDLL(ceilings.PROBE_LIB_PATH)
+    assert all(hasattr(probe_lib, n) for n in probe_names)
 
 
 def test_binding_structs_match_header(tmp_path):
@@ -56,7 +63,7 @@ def test_probe_rejects_unsupported_arguments():
     # Checked before any HIP call, so this runs without a GPU.
     for kind, param in (("valu", 3), ("exp2", 0), ("loads_l2", 5), ("mfma_random", 1), ("chains", 3), ("chains", 0)):
         with pytest.raises(d.DINOv3Error, match="unsupported probe"):
-            d.probe(kind, param)
+            ceilings.probe(kind, param)
 
 
 def test_constants_match_reference():

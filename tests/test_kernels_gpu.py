@@ -12,6 +12,7 @@ import numpy as np
 import pytest
 
 import dinov3_hrx as d
+from dinov3_hrx import ceilings
 import oracle
 
 from conftest import cosine, from_frag, to_frag
@@ -706,11 +707,17 @@ def test_gemm_bitwise_repeatable(eng, kernel, shape):
         assert np.array_equal(first, again), f"{kernel}: launch {rep + 2} differs in {int((first != again).sum())} elements"
 
 
-@pytest.mark.parametrize("shape", ["b64", "512b8"])
+ATTN_SHAPES = {**SHAPES, "384b8": (8, 24)}
+
+
+@pytest.mark.parametrize("shape", ["b64", "512b8", "384b8"])
 def test_attention_bitwise_repeatable(eng, shape):
-    # T = 201 runs the unrolled 32-key-block loop, T = 1029 the run-time
-    # 64-key-block loop; both DMA K/V two blocks ahead into three buffers.
-    images, grid = SHAPES[shape]
+    # T = 201 runs attention_kernel<7> (seven 32-key blocks, unrolled),
+    # T = 1029 attention_split_kernel<17> (two key halves of 17 unrolled
+    # 32-key blocks), T = 581 (384x384) attention_kernel<0>, the run-time
+    # count of 64-key blocks that serves every other image size; all three
+    # DMA K/V two blocks ahead into three buffers.
+    images, grid = ATTN_SHAPES[shape]
     rng = np.random.default_rng(12)
     T = grid * grid + 5
     tpad = (T + 127) // 128 * 128
@@ -771,14 +778,14 @@ def test_machine_ceiling_probes():
     # One wave per SIMD issues independent 32x32x16 f16 MFMAs every 32 cycles
     # (8 per 256), and 2 L1-resident 16-byte loads per 8 MFMAs leave that
     # rate intact; the implied clock is a plausible shader clock.
-    r = d.probe("mfma_random")
+    r = ceilings.probe("mfma_random")
     assert 250 <= r["cycles_per_8_mfma"] <= 270, r
     assert 0.5 <= r["clock_ghz"] <= 2.6, r
     assert r["tflops"] > 0.5 * 2500 * r["clock_ghz"] / 2.4, r
-    l1 = d.probe("loads_l1", 2)
+    l1 = ceilings.probe("loads_l1", 2)
     assert l1["cycles_per_8_mfma"] <= 1.1 * r["cycles_per_8_mfma"], l1
     # Eight independent accumulators issue at the full rate; one chain of
     # dependent MFMAs can be no faster.
-    c8, c1 = d.probe("chains", 8), d.probe("chains", 1)
+    c8, c1 = ceilings.probe("chains", 8), ceilings.probe("chains", 1)
     assert 250 <= c8["cycles_per_8_mfma"] <= 270, c8
     assert c1["cycles_per_8_mfma"] >= c8["cycles_per_8_mfma"] - 1, c1

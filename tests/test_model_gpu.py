@@ -2,7 +2,8 @@
 restated on seeded random-init weights, plus the configs of BASELINE.json).
 
 Parity bar: all-token and CLS cosine against the float64 oracle > 0.9999
-(tests/model.rs:85-86), max-abs error printed; batched vs single-image
+(tests/model.rs:85-86) and max-abs error within a per-preset ceiling
+(MAX_ABS below); batched vs single-image
 cosine > 0.99999 (tests/model.rs:87-93); bitwise determinism of a repeated
 batched forward (tests/model.rs:95)."""
 import os
@@ -38,11 +39,23 @@ def models(weight_file):
         m.close()
 
 
-def compare(got, want, what):
+# Max-abs ceilings against the float64 oracle, per weight preset. Measured
+# on the MI355X: about 1.8e-3 on the BASELINE preset (0) and 0.0106-0.0137 on
+# the stress preset (1) over every image size and batch tested; the ceilings
+# leave about 1.5-3x of margin, so an accuracy regression that keeps the
+# cosine above 0.9999 (tests/model.rs:79-86) still fails here.
+MAX_ABS = {0: 0.005, 1: 0.02}
+
+
+def compare(got, want, what, preset):
+    """All-token and CLS cosine > 0.9999 and max-abs within the preset's
+    ceiling; prints the three figures."""
     got = np.asarray(got, np.float64)
-    err = np.abs(got - want).max()
+    err = float(np.abs(got - want).max())
     c_all, c_cls = cosine(got, want), cosine(got[0], want[0])
-    print(f"{what}: all-token cos {c_all:.7f}  CLS cos {c_cls:.7f}  max-abs {err:.4g}")
+    print(f"{what}: all-token cos {c_all:.7f}  CLS cos {c_cls:.7f}  max-abs {err:.4g} (ceiling {MAX_ABS[preset]})")
+    assert c_all > 0.9999 and c_cls > 0.9999, what
+    assert err <= MAX_ABS[preset], f"{what}: max-abs {err:.4g} above {MAX_ABS[preset]}"
     return c_all, c_cls, err
 
 
@@ -54,8 +67,7 @@ def test_forward_matches_oracle(models, oracle_weights, preset):
     assert out.shape == (2, 201, 384) and out.dtype == np.float32
     for i in range(2):
         want = oracle.forward(oracle_weights(preset), px[i], 14)
-        c_all, c_cls, _ = compare(out[i], want, f"preset {preset} image {i}")
-        assert c_all > 0.9999 and c_cls > 0.9999
+        compare(out[i], want, f"preset {preset} image {i}", preset)
 
 
 def test_acceptance_pattern_and_changing_batch(models, oracle_weights):
@@ -67,8 +79,7 @@ def test_acceptance_pattern_and_changing_batch(models, oracle_weights):
         img = images[i * d.IMAGE_ELEMENTS:(i + 1) * d.IMAGE_ELEMENTS]
         got = m.forward(img)[0]
         want = oracle.forward(oracle_weights(1), img, 14)
-        c_all, c_cls, _ = compare(got, want, f"acceptance image {i}")
-        assert c_all > 0.9999 and c_cls > 0.9999
+        compare(got, want, f"acceptance image {i}", 1)
         assert cosine(batched[i], got) > 0.99999
     assert np.array_equal(m.forward(images), batched)  # bitwise determinism
     with pytest.raises(d.DINOv3Error, match="complete 3×224×224 images"):
@@ -124,8 +135,7 @@ def test_full_batch_64_rows_independent_of_batch(models, oracle_weights):
     assert np.array_equal(out[:2], m.forward(px[:2]))
     assert np.array_equal(out[62:], m.forward(px[62:]))
     for i in (0, 63):
-        c_all, c_cls, _ = compare(out[i], oracle.forward(oracle_weights(0), px[i], 14), f"b64 image {i}")
-        assert c_all > 0.9999 and c_cls > 0.9999
+        compare(out[i], oracle.forward(oracle_weights(0), px[i], 14), f"b64 image {i}", 0)
 
 
 def test_batch_32_stress_matches_oracle(models, oracle_weights):
@@ -139,8 +149,7 @@ def test_batch_32_stress_matches_oracle(models, oracle_weights):
     out = m.forward(px)
     assert out.shape == (32, 201, 384) and np.all(np.isfinite(out))
     for i in (0, 15, 16, 31):
-        c_all, c_cls, _ = compare(out[i], oracle.forward(oracle_weights(1), px[i], 14), f"b32 stress image {i}")
-        assert c_all > 0.9999 and c_cls > 0.9999
+        compare(out[i], oracle.forward(oracle_weights(1), px[i], 14), f"b32 stress image {i}", 1)
     assert np.array_equal(out[:2], m.forward(px[:2]))
     assert np.array_equal(out[30:], m.forward(px[30:]))
 
@@ -156,8 +165,7 @@ def test_batch_64_stress_every_grouping(models, oracle_weights):
     out = m.forward(px)
     assert out.shape == (64, 201, 384) and np.all(np.isfinite(out))
     for i in (0, 21, 42, 63):
-        c_all, c_cls, _ = compare(out[i], oracle.forward(oracle_weights(1), px[i], 14), f"b64 stress image {i}")
-        assert c_all > 0.9999 and c_cls > 0.9999
+        compare(out[i], oracle.forward(oracle_weights(1), px[i], 14), f"b64 stress image {i}", 1)
     try:
         for n in (1, 2, 4):
             m.set_branches(n)
@@ -179,8 +187,7 @@ def test_512_batch_8_grouped_plan(models, oracle_weights):
     out = m.forward(px)
     assert out.shape == (8, 1029, 384) and np.all(np.isfinite(out))
     for i in (0, 7):
-        c_all, c_cls, _ = compare(out[i], oracle.forward(oracle_weights(1), px[i], 32), f"512 b8 image {i}")
-        assert c_all > 0.9999 and c_cls > 0.9999
+        compare(out[i], oracle.forward(oracle_weights(1), px[i], 32), f"512 b8 image {i}", 1)
     try:
         m.set_branches(1)
         assert np.array_equal(m.forward(px), out)
@@ -217,8 +224,7 @@ def test_half_precision_checkpoints(models, tmp_path, weight_file, dtype):
         assert np.array_equal(got, mf.forward(px))
     ow = oracle.Weights(widened)
     for i in range(2):
-        c_all, c_cls, _ = compare(got[i], oracle.forward(ow, px[i], 14), f"{dtype} checkpoint image {i}")
-        assert c_all > 0.9999 and c_cls > 0.9999
+        compare(got[i], oracle.forward(ow, px[i], 14), f"{dtype} checkpoint image {i}", 1)
 
 
 @pytest.mark.parametrize("preset", [0, 1])
@@ -234,9 +240,8 @@ def test_layernorm_fusion_matches_unfused_plan(models, oracle_weights, preset):
     for i in range(8):
         assert cosine(fused[i], plain[i]) > 0.99999
     want = oracle.forward(oracle_weights(preset), px[0], 14)
-    c_all, c_cls, _ = compare(plain[0], want, f"unfused plan preset {preset}")
-    assert c_all > 0.9999 and c_cls > 0.9999
-    compare(fused[0], want, f"fused plan preset {preset}")
+    compare(plain[0], want, f"unfused plan preset {preset}", preset)
+    compare(fused[0], want, f"fused plan preset {preset}", preset)
 
 
 def test_branches_are_bitwise_identical(models):
@@ -289,8 +294,7 @@ def test_512_high_resolution(models, oracle_weights, preset):
     px = d.random_pixels(1, 1, 512)
     out = m.forward(px)
     assert out.shape == (1, 1029, 384)
-    c_all, c_cls, _ = compare(out[0], oracle.forward(oracle_weights(preset), px[0], 32), f"512 preset {preset}")
-    assert c_all > 0.9999 and c_cls > 0.9999
+    compare(out[0], oracle.forward(oracle_weights(preset), px[0], 32), f"512 preset {preset}", preset)
 
 
 @pytest.mark.parametrize("size", [16, 64, 256, 384])
@@ -307,8 +311,7 @@ def test_other_image_sizes(models, oracle_weights, size):
     out = m.forward(px)
     assert out.shape == (2, G * G + 5, 384)
     for i in range(2):
-        c_all, c_cls, _ = compare(out[i], oracle.forward(oracle_weights(1), px[i], G), f"{size}x{size} image {i}")
-        assert c_all > 0.9999 and c_cls > 0.9999
+        compare(out[i], oracle.forward(oracle_weights(1), px[i], G), f"{size}x{size} image {i}", 1)
     assert np.array_equal(m.forward(px[1:]), out[1:])
 
 
@@ -319,8 +322,7 @@ def test_largest_image_size(models, oracle_weights):
     assert m.tokens == 4101
     px = d.random_pixels(1024, 1, 1024)
     out = m.forward(px)
-    c_all, c_cls, _ = compare(out[0], oracle.forward(oracle_weights(1), px[0], 64), "1024x1024")
-    assert c_all > 0.9999 and c_cls > 0.9999
+    compare(out[0], oracle.forward(oracle_weights(1), px[0], 64), "1024x1024", 1)
 
 
 def test_benchmark(models):
