@@ -14,7 +14,10 @@ using gemm::tiles_for;
 // 128x128 tiles to fill 256 CUs) use 128x64 tiles, twice as many workgroups
 // of a quarter of the registers.
 using PatchTile = Tile<64, 128, 2, 2>;
-using QkvTile = Tile<128, 128, 4, 1>;
+// QKV on 32-deep stages (24 KB of weight buffers; its RoPE angles wait in
+// LDS, not registers): four workgroups per CU, so a batch of 64 (909 tiles)
+// runs as one round of workgroups.
+using QkvTile = Tile<128, 128, 4, 1, 32>;
 using ResidTile = Tile<128, 64, 4, 1>;
 using ResidTileK = Tile<128, 64, 4, 1, 128>;  // down projection (k = 1536)
 using SwigluTile = Tile<256, 128, 4, 1, 64>;
@@ -46,8 +49,11 @@ hipError_t launch_patch_embed(const PatchEmbedArgs& a, hipStream_t s) {
 
 hipError_t launch_qkv_rope(const QkvArgs& a, hipStream_t s) {
     const int tiles = tiles_for<QkvTile>(a.images * (a.grid * a.grid + kPrefix), 3 * kHidden);
-    return a.stats ? launch<QkvTile>(gemm::qkv_rope_kernel<QkvTile, true>, tiles, a, s)
-                   : launch<QkvTile>(gemm::qkv_rope_kernel<QkvTile, false>, tiles, a, s);
+    const dim3 grid(gemm::tile_grid(tiles));
+    const size_t lds = gemm::rope_lds_bytes(a.grid);
+    if (a.stats) hipLaunchKernelGGL((gemm::qkv_rope_kernel<QkvTile, true>), grid, dim3(QkvTile::THREADS), lds, s, a);
+    else hipLaunchKernelGGL((gemm::qkv_rope_kernel<QkvTile, false>), grid, dim3(QkvTile::THREADS), lds, s, a);
+    return hipGetLastError();
 }
 
 hipError_t launch_resid(const ResidArgs& a, hipStream_t s) {

@@ -143,23 +143,55 @@ __device__ __forceinline__ void init_frags(ActFrags<T> (&al)[2], const half_t* a
     }
 }
 
+// RoPE angles in LDS. DINOv3's tables are separable (weights.rs:127-144):
+// the angle of channel c < 16 of patch (gy, gx) depends on gy only, that of
+// channel 16 <= c < 32 on gx only, and channels 32..63 repeat 0..31. Four
+// [R][16] float tables (R = the grid side rounded up to 16) hold every angle
+// the QKV epilogue needs: cos and sin of the row part (table row gy, from
+// patch (gy, 0) of the full [P][64] tables) and of the column part (table
+// row gx, from patch (0, gx)), the same float values the full tables hold.
+__host__ __device__ constexpr int rope_table_rows(int grid) { return (grid + 15) / 16 * 16; }
+__host__ __device__ constexpr int rope_lds_bytes(int grid) { return 4 * rope_table_rows(grid) * 16 * 4; }
+
+// Wave w (0..3) fills table w (cos row part, sin row part, cos column part,
+// sin column part) with DMA loads of 16 table rows each: lane i moves 16
+// bytes, channels 4(i % 4) .. +3 of table row 16q + i / 4, to LDS byte
+// 16i of the load's 1 KB. Rows past the grid read beyond the source table's
+// bounds, which the buffer descriptor turns into zeros, or other patches'
+// angles (grids under 16), and are never read back.
+__device__ __forceinline__ void rope_table_dma(const float* cos, const float* sin, int grid, float* lds, int tid) {
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int rows = rope_table_rows(grid);
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(wave & 1 ? sin : cos), 0, grid * grid * kHeadDim * 4, kBufferRsrcWord3);
+    float* const table = lds + wave * rows * 16;
+    for (int q = 0; q < rows / 16; ++q) {  // uniform, 1..4
+        const int row = q * 16 + (lane >> 2);
+        const int src = (wave < 2 ? row * grid * kHeadDim : row * kHeadDim + 16) + (lane & 3) * 4;  // floats
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(table + q * 256), 16,
+                                                 src * 4, 0, 0, 0);
+    }
+}
+
 // QKV + bias + 2D RoPE. A wave's 128 columns are two heads of q, k or v (a
 // 128-column tile never straddles two of them); channel c and its rotation
 // partner c+32 of a head are acc.v[2h] / acc.v[2h+1] of the same lane, and
 // both use angle column c of the RoPE tables (DINOv3's tables repeat columns
-// 0..31 in 32..63; only the first half is read). Results are rounded to f16
-// and regrouped in registers (frag_swap) so each lane holds 8 consecutive
-// channels of its row. q, k and v are [image][head] matrices of tpad rows x
-// 64 channels, each in fragment order: a lane's 8 channels are one 16-byte
-// piece of a fragment, so the 64 lanes of a store cover one or two runs of
-// whole rows' pieces per half-fragment (a row-major head row would take 32
-// separate 32-byte writes per store instead).
+// 0..31 in 32..63; only the first half is read, from the LDS tables of
+// rope_table_dma). Results are rounded to f16 and regrouped in registers
+// (frag_swap) so each lane holds 8 consecutive channels of its row. q, k
+// and v are [image][head] matrices of tpad rows x 64 channels, each in
+// fragment order: a lane's 8 channels are one 16-byte piece of a fragment,
+// so the 64 lanes of a store cover one or two runs of whole rows' pieces per
+// half-fragment (a row-major head row would take 32 separate 32-byte writes
+// per store instead). Launched with rope_lds_bytes(grid) of dynamic LDS.
 template <class T, bool LN>
-__global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void qkv_rope_kernel(QkvArgs p) {
+__global__ __launch_bounds__(T::THREADS, T::FM == 1 ? (T::BK == 32 ? 4 : 3) : 2) void qkv_rope_kernel(QkvArgs p) {
     static_assert(T::TN == 2 * kHeadDim && T::WGN == 1, "two heads per wave, whole rows per wave");
     __shared__ __attribute__((aligned(16))) half_t wb0[T::WF_HALFS], wb1[T::WF_HALFS], wb2[T::WF_HALFS];
     __shared__ __attribute__((aligned(16))) float cst[2][T::BN];  // bias, wsum of the tile's columns
     __shared__ float2_t rows_norm[T::BM];                          // (mean, rstd) of the tile's rows
+    extern __shared__ __attribute__((aligned(16))) float rope_lds[];  // rope_table_dma's four tables
     static_assert(T::BN <= T::THREADS, "one thread per column constant");
     const int P = p.grid * p.grid, Tok = P + kPrefix, M = p.images * Tok;
     constexpr int NT = 3 * kHidden / T::BN;
@@ -167,34 +199,17 @@ __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void qkv_rope_kerne
     ActFrags<T> al[2];
     init_frags(al, p.h, M, kHidden);
     WeightDma<T> wd(p.w, 3 * kHidden, kHidden);
-    // The epilogue's own operands are loaded ahead of the K loop: the tile's
-    // column constants and its rows' LayerNorm (mean, rstd), which wait in
-    // LDS, and each row's RoPE angles (cos, sin of channels 8g + 4hi .. +3,
-    // g = 0..3), which wait in registers. v tiles and prefix rows rotate by
-    // cos 1, sin 0.
+    // The epilogue's own operands are loaded ahead of the K loop: the RoPE
+    // tables (DMA, first: they are the oldest loads every later wait covers),
+    // the tile's column constants and its rows' LayerNorm (mean, rstd), all
+    // of which wait in LDS.
     float4_t raw[T::FM][3];
-    float4_t rco[T::FM][4], rsi[T::FM][4];
     float cb = 0.f, cw = 0.f;
     gemm_tile_dma<T, 1, kHidden / T::BK>(
         al, wd, wb0, wb1, wb2, NT, NT * ((M + T::BM - 1) / T::BM), kHidden / T::BK,
         [&](int m0, int n0) {
+            rope_table_dma(p.cos, p.sin, p.grid, rope_lds, tid);
             const Frag<T> f(m0, n0);
-            const int part = f.n_base / kHidden;
-#pragma unroll
-            for (int j = 0; j < T::FM; ++j) {
-                const int m = min(f.row(j), M - 1);
-                const int tok = m - m / Tok * Tok;
-                const size_t angle_row = (size_t)max(tok - kPrefix, 0) * kHeadDim;
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    rco[j][g] = float4_t{1.f, 1.f, 1.f, 1.f};
-                    rsi[j][g] = float4_t{};
-                    if (part < 2 && tok >= kPrefix) {
-                        rco[j][g] = ld4(p.cos + angle_row + g * 8 + f.hi * 4);
-                        rsi[j][g] = ld4(p.sin + angle_row + g * 8 + f.hi * 4);
-                    }
-                }
-            }
             if constexpr (LN) {
 #pragma unroll
                 for (int j = 0; j < T::FM; ++j) {
@@ -228,6 +243,7 @@ __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void qkv_rope_kerne
         const int part = f.n_base / kHidden, head0 = (f.n_base % kHidden) / kHeadDim;
         half_t* const out = part == 0 ? p.q : part == 1 ? p.k : p.v;
         const size_t head_elems = (size_t)p.tpad * kHeadDim;
+        const int rows16 = rope_table_rows(p.grid);
         // The tile's rows lie in images img0 .. img0 + BM / Tok + 1 (img0
         // from the tile origin, so it is uniform); the descriptor covers
         // those.
@@ -239,8 +255,18 @@ __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? 3 : 2) void qkv_rope_kerne
             const int mr = f.row(j);
             const int m = min(mr, M - 1);  // rows past M are computed but never written out
             const int img = m / Tok, tok = m - img * Tok;
-            const float4_t* const co = rco[j];
-            const float4_t* const si = rsi[j];
+            // This row's angles (cos, sin of channels 8g + 4hi .. +3, g =
+            // 0..3); v tiles and prefix rows rotate by cos 1, sin 0.
+            const bool rot = part < 2 && tok >= kPrefix;
+            const int pt = max(tok - kPrefix, 0), gy = pt / p.grid, gx = pt - gy * p.grid;
+            float4_t co[4], si[4];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int at = (g < 2 ? gy * 16 : 2 * rows16 * 16 + gx * 16) + (g & 1) * 8 + f.hi * 4;
+                const float4_t c4 = *(const float4_t*)&rope_lds[at], s4 = *(const float4_t*)&rope_lds[at + rows16 * 16];
+                co[g] = rot ? c4 : float4_t{1.f, 1.f, 1.f, 1.f};
+                si[g] = rot ? s4 : float4_t{};
+            }
             RowNorm rn{0.f, 1.f};
             if constexpr (LN) {
                 const float2_t v = rows_norm[f.m_base - m0 + j * 32 + f.l32];
