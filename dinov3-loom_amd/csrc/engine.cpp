@@ -315,6 +315,15 @@ void release_staging(dhx_engine* e) {
     e->pin_in_bytes = e->pin_out_bytes = 0;
 }
 
+void check_slot(const dhx_engine* e, uint32_t slot) {
+    if (slot >= DHX_STAGING_SLOTS) throw dhx::Error("staging slot must be 0 or 1");
+    if (!e->up) throw dhx::Error("staging was not reserved");
+}
+
+}  // namespace
+
+namespace dhx {
+
 // memcpy split over host threads: pageable <-> pinned copies of tens of MB
 // run at a few GB/s on one core, far below the PCIe link.
 void parallel_copy(void* dst, const void* src, uint64_t n) {
@@ -335,15 +344,6 @@ void parallel_copy(void* dst, const void* src, uint64_t n) {
     for (auto& th : pool) th.join();
 }
 
-void check_slot(const dhx_engine* e, uint32_t slot) {
-    if (slot >= DHX_STAGING_SLOTS) throw dhx::Error("staging slot must be 0 or 1");
-    if (!e->up) throw dhx::Error("staging was not reserved");
-}
-
-}  // namespace
-
-namespace dhx {
-
 uint32_t engine_external(dhx_engine* e, void* ptr, uint64_t bytes) {
     e->buffers.push_back(ptr);
     e->sizes.push_back(bytes);
@@ -362,6 +362,48 @@ void engine_queue(dhx_engine* e, const dhx_launch* launches, size_t n, hipStream
     for (size_t i = 0; i < n; ++i) validate(e, launches[i]);
     set_device(e);
     for (size_t i = 0; i < n; ++i) hip_check(e, launch_one(e, launches[i], stream), "kernel launch");
+}
+
+void* engine_staging_in(dhx_engine* e, uint32_t slot) {
+    check_slot(e, slot);
+    return e->pin_in[slot];
+}
+
+void* engine_staging_out(dhx_engine* e, uint32_t slot) {
+    check_slot(e, slot);
+    return e->pin_out[slot];
+}
+
+uint64_t engine_staging_in_bytes(const dhx_engine* e) { return e->pin_in_bytes; }
+
+uint64_t engine_staging_out_bytes(const dhx_engine* e) { return e->pin_out_bytes; }
+
+void engine_wait_upload(dhx_engine* e, uint32_t slot) {
+    ensure_usable(e);
+    check_slot(e, slot);
+    set_device(e);
+    hip_check(e, hipEventSynchronize(e->in_done[slot]), "upload wait");
+}
+
+void engine_upload(dhx_engine* e, dhx_region dst, uint64_t n, uint32_t slot) {
+    ensure_usable(e);
+    check_slot(e, slot);
+    check_region(e, dst);
+    if (n > dst.bytes) throw Error("input exceeds allocated region");
+    if (n > e->pin_in_bytes) throw Error("input exceeds reserved staging");
+    set_device(e);
+    // dst is the slot's device input, which the graph last replayed for this
+    // slot may still be reading.
+    hip_check(e, hipStreamWaitEvent(e->up, e->graph_done[slot], 0), "hipStreamWaitEvent");
+    hip_check(e, hipMemcpyAsync(region_ptr(e, dst), e->pin_in[slot], n, hipMemcpyHostToDevice, e->up), "upload");
+    hip_check(e, hipEventRecord(e->in_done[slot], e->up), "hipEventRecord");
+}
+
+void engine_wait_readback(dhx_engine* e, uint32_t slot) {
+    ensure_usable(e);
+    check_slot(e, slot);
+    set_device(e);
+    hip_check(e, hipEventSynchronize(e->out_done[slot]), "readback wait");
 }
 
 hipStream_t engine_stream(const dhx_engine* e) { return e->stream; }
@@ -623,18 +665,10 @@ int dhx_reserve_staging(dhx_engine* e, uint64_t in_bytes, uint64_t out_bytes) {
 
 int dhx_copy_in(dhx_engine* e, dhx_region dst, const void* src, uint64_t n, uint32_t slot) {
     return guarded(e, [&] {
-        ensure_usable(e);
-        check_slot(e, slot);
-        check_region(e, dst);
-        if (n > dst.bytes) throw dhx::Error("input exceeds allocated region");
-        if (n > e->pin_in_bytes) throw dhx::Error("input exceeds reserved staging");
         if (n && !src) throw dhx::Error("null input");
-        set_device(e);
-        hip_check(e, hipEventSynchronize(e->in_done[slot]), "upload wait");  // staging buffer free again
-        parallel_copy(e->pin_in[slot], src, n);
-        hip_check(e, hipStreamWaitEvent(e->up, e->graph_done[slot], 0), "hipStreamWaitEvent");
-        hip_check(e, hipMemcpyAsync(region_ptr(e, dst), e->pin_in[slot], n, hipMemcpyHostToDevice, e->up), "upload");
-        hip_check(e, hipEventRecord(e->in_done[slot], e->up), "hipEventRecord");
+        dhx::engine_wait_upload(e, slot);  // staging buffer free again
+        dhx::parallel_copy(e->pin_in[slot], src, n);
+        dhx::engine_upload(e, dst, n, slot);
     });
 }
 
@@ -669,13 +703,10 @@ int dhx_copy_out(dhx_engine* e, dhx_region src, uint64_t n, uint32_t slot) {
 
 int dhx_copy_out_finish(dhx_engine* e, void* dst, uint64_t n, uint32_t slot) {
     return guarded(e, [&] {
-        ensure_usable(e);
-        check_slot(e, slot);
         if (n > e->pin_out_bytes) throw dhx::Error("output exceeds reserved staging");
         if (n && !dst) throw dhx::Error("null output");
-        set_device(e);
-        hip_check(e, hipEventSynchronize(e->out_done[slot]), "readback wait");
-        parallel_copy(dst, e->pin_out[slot], n);
+        dhx::engine_wait_readback(e, slot);
+        dhx::parallel_copy(dst, e->pin_out[slot], n);
     });
 }
 

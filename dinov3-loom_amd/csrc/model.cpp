@@ -5,8 +5,10 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <condition_variable>
 #include <cstdlib>
 #include <cstring>
+#include <deque>
 #include <map>
 #include <memory>
 #include <mutex>
@@ -141,6 +143,68 @@ void* scratch_address(int device) {
     return scratch_slot_locked(device).ptr;
 }
 
+// Host copies between pageable and pinned memory (each split over threads
+// by parallel_copy), run one after another on a thread of their own in the
+// order they are submitted. It never calls the HIP runtime: HIP calls from
+// another thread beside a graph launch were measured to slow the launch
+// down, so the thread that launches keeps every HIP call and hands the
+// copies over.
+class Copier {
+public:
+    Copier() : worker_([this] { run(); }) {}
+    ~Copier() {
+        {
+            std::lock_guard<std::mutex> lock(m_);
+            stop_ = true;
+        }
+        work_.notify_all();
+        worker_.join();  // queued copies still run: their buffers outlive the caller's scope
+    }
+    Copier(const Copier&) = delete;
+    Copier& operator=(const Copier&) = delete;
+
+    // Queues dst <- src (n bytes); returns the copy's ticket.
+    uint64_t submit(void* dst, const void* src, uint64_t n) {
+        std::lock_guard<std::mutex> lock(m_);
+        jobs_.push_back(Job{dst, src, n});
+        work_.notify_all();
+        return submitted_++;
+    }
+
+    // Waits until the copy with this ticket (and every earlier one) is done.
+    void wait(uint64_t ticket) {
+        std::unique_lock<std::mutex> lock(m_);
+        done_cv_.wait(lock, [&] { return done_ > ticket; });
+    }
+
+private:
+    struct Job {
+        void* dst;
+        const void* src;
+        uint64_t n;
+    };
+    void run() {
+        std::unique_lock<std::mutex> lock(m_);
+        for (;;) {
+            work_.wait(lock, [&] { return stop_ || !jobs_.empty(); });
+            if (jobs_.empty()) return;  // stopping, nothing left
+            const Job j = jobs_.front();
+            jobs_.pop_front();
+            lock.unlock();
+            dhx::parallel_copy(j.dst, j.src, j.n);
+            lock.lock();
+            ++done_;
+            done_cv_.notify_all();
+        }
+    }
+    std::mutex m_;
+    std::condition_variable work_, done_cv_;
+    std::deque<Job> jobs_;
+    uint64_t submitted_ = 0, done_ = 0;
+    bool stop_ = false;
+    std::thread worker_;  // last: starts once the members above exist
+};
+
 constexpr uint64_t align256(uint64_t v) { return (v + 255) & ~255ull; }
 
 // Finite check of the whole input before any GPU work (lib.rs validates
@@ -237,10 +301,12 @@ public:
     }
 
     // lib.rs:90-114: chunks of max_batch images, pipelined over the two
-    // transfer slots: chunk i uses slot i % 2, so its host copy and upload
-    // run while chunk i-1's graph runs, and chunk i-1's readback and host
-    // copy while chunk i's graph runs. Results are those of the chunks run
-    // one at a time.
+    // transfer slots: chunk i uses slot i % 2. This thread issues every HIP
+    // call (uploads, graph launches, readbacks) and a Copier thread does the
+    // host copies into and out of the pinned staging buffers, each handed
+    // over as soon as its buffer is free: chunk i+1's input copy and chunk
+    // i-1's output copy run while chunk i is launched and computed. Results
+    // are those of the chunks run one at a time.
     void forward(const float* pixels, uint64_t n, float* out, uint64_t out_floats) {
         check_input(pixels, n);
         const uint64_t batch = n / image_elems_;
@@ -252,21 +318,42 @@ public:
         auto size_of = [&](uint64_t i) { return std::min<uint64_t>(opts_.max_batch, batch - i * opts_.max_batch); };
         for (uint64_t i = 0; i < std::min<uint64_t>(chunks, 2); ++i) prepare(size_of(i), (uint32_t)(i & 1));
         if (chunks > 2) prepare(size_of(chunks - 1), (uint32_t)((chunks - 1) & 1));  // the tail chunk
-        for (uint64_t i = 0; i <= chunks; ++i) {
-            if (i < chunks) {
-                const uint32_t slot = (uint32_t)(i & 1);
-                const uint64_t b = size_of(i), first = i * opts_.max_batch;
-                check(dhx_copy_in(e, a_[image_buffer(slot)], pixels + first * image_elems_, b * image_elems_ * 4, slot), e);
-                check(dhx_replay_slot(e, key(b, slot), slot), e);
-                check(dhx_copy_out(e, a_[out_buffer(slot)], b * per_image * 4, slot), e);
-            }
-            if (i > 0) {
-                const uint64_t j = i - 1;
-                check(dhx_copy_out_finish(e, out + j * opts_.max_batch * per_image, size_of(j) * per_image * 4,
-                                          (uint32_t)(j & 1)),
-                      e);
-            }
+        auto in_bytes = [&](uint64_t i) { return size_of(i) * image_elems_ * 4; };
+        auto out_bytes = [&](uint64_t i) { return size_of(i) * per_image * 4; };
+        if (in_bytes(0) > dhx::engine_staging_in_bytes(e) || out_bytes(0) > dhx::engine_staging_out_bytes(e))
+            throw Error("chunk exceeds reserved staging");
+        std::vector<uint64_t> filled(chunks), drained(chunks);
+        Copier copier;
+        // Chunk i's pixels into slot i % 2's input staging, once the slot's
+        // previous upload has left it.
+        auto fill = [&](uint64_t i) {
+            const uint32_t slot = (uint32_t)(i & 1);
+            dhx::engine_wait_upload(e, slot);
+            filled[i] = copier.submit(dhx::engine_staging_in(e, slot), pixels + i * opts_.max_batch * image_elems_,
+                                      in_bytes(i));
+        };
+        // Chunk i's tokens out of slot i % 2's output staging, once its
+        // readback has landed there.
+        auto drain = [&](uint64_t i) {
+            const uint32_t slot = (uint32_t)(i & 1);
+            dhx::engine_wait_readback(e, slot);
+            drained[i] = copier.submit(out + i * opts_.max_batch * per_image, dhx::engine_staging_out(e, slot),
+                                       out_bytes(i));
+        };
+        fill(0);
+        if (chunks > 1) fill(1);
+        for (uint64_t i = 0; i < chunks; ++i) {
+            const uint32_t slot = (uint32_t)(i & 1);
+            copier.wait(filled[i]);
+            dhx::engine_upload(e, a_[image_buffer(slot)], in_bytes(i), slot);
+            if (i >= 2) copier.wait(drained[i - 2]);  // the slot's output staging is read out
+            check(dhx_replay_slot(e, key(size_of(i), slot), slot), e);
+            check(dhx_copy_out(e, a_[out_buffer(slot)], out_bytes(i), slot), e);
+            if (i >= 1 && i + 1 < chunks) fill(i + 1);  // its slot last held chunk i-1, uploaded by now
+            if (i >= 1) drain(i - 1);
         }
+        drain(chunks - 1);
+        copier.wait(drained[chunks - 1]);
     }
 
     // Upload one chunk and replay its graph (recording it on first use).
