@@ -15,7 +15,12 @@ kernel, in the code the compiler actually emitted (a reordering by the
 compiler or by a later edit of the K loop would break it silently, showing
 only as rare run-to-run differences on the GPU). A negative control plants
 the mistake in a copy of the GEMM core (the step's DMA issued before its
-register loads) and checks that the test would catch it."""
+register loads) and checks that the test would catch it.
+
+A second check on the same assembly: the attention kernels touch global
+memory only through 16-byte Q fragment loads, buffer (DMA) loads and buffer
+stores; everything else, such as the split-key kernel's hand-over between
+its key halves, stays in LDS."""
 import os
 import re
 import shutil
@@ -120,3 +125,21 @@ def test_the_check_catches_dma_issued_before_register_loads(hipcc, tmp_path):
     print(f"{len(caught)} of {len(kernels)} GEMM kernels flagged")
     for kernel in ("qkv_rope_kernel", "resid_kernel", "swiglu_kernel", "splitk_kernel"):
         assert any(kernel in name for name in caught), kernel
+
+
+def test_attention_kernels_touch_global_memory_only_as_designed(hipcc, tmp_path):
+    # A form of the split-key kernel's merge (its LDS buffers picked through
+    # pointer tables declared inside a lambda's `if constexpr` branches) came
+    # out of this compiler as 32-bit global stores and loads near address 0,
+    # which fault on the GPU; every attention kernel is held to the designed
+    # set of global-memory instructions (Q fragments as 16-byte loads, K and V
+    # as DMA loads, the output as 16-byte buffer stores).
+    kernels = assembly(os.path.join(KERNELS, "attention.hip"), str(tmp_path / "attention.s"), KERNELS)
+    assert any("attention_split_kernel" in k for k in kernels)
+    for name, ins in kernels.items():
+        for i in ins:
+            op = i.split()[0]
+            if op.startswith(("global_", "flat_", "scratch_")):
+                assert op == "global_load_dwordx4", f"{name}: {i}"
+            elif op.startswith("buffer_store"):
+                assert op == "buffer_store_dwordx4", f"{name}: {i}"
