@@ -21,10 +21,15 @@ using QkvTile = Tile<128, 128, 4, 1, 32>;
 using ResidTile = Tile<128, 64, 4, 1>;
 using ResidTileK = Tile<128, 64, 4, 1, 128>;  // down projection (k = 1536)
 using SwigluTile = Tile<256, 128, 4, 1, 64>;
-// SwiGLU for launches of fewer rows (batch 32 as two image groups, small
-// batches): 128-row tiles, three workgroups per CU instead of two.
+// SwiGLU for launches of fewer rows (batch 32's and 512x512 batch 8's image
+// groups of 3216 and 4116 rows, small batches): 128-row tiles, three
+// workgroups per CU instead of two. Measured in the two-group forward: the
+// 128-row tiles win at 3216 and 4116 rows (at 4116 the 256-row tiling's
+// last tile holds 20 rows), the 256-row ones at 6432 (batch 64's groups).
 using SwigluTileS = Tile<128, 128, 4, 1, 64>;
-constexpr int kSwigluSmallRows = 4096;
+constexpr int kSwigluSmallRows = 5120;
+// Launches of up to this many rows take four XCD N slices, larger ones two.
+constexpr int kSwigluSplit4Rows = 8192;
 // The folded LayerNorm's -mean * wsum term joins column block i's
 // accumulators at K step i + 1, so where it enters the fp32 sum depends on
 // the stage depth. Both tile shapes must share it for a row's result to be
@@ -89,12 +94,12 @@ static hipError_t launch_swiglu_tiles(const SwigluArgs& a, hipStream_t s) {
 }
 
 // The XCD split (each XCD's L2 keeps 1/NS of the weights): two N slices for
-// the whole batch-64 launch, four for the image groups of 4096 - 8191 rows
+// the whole batch-64 launch, four for the image groups of 5120 - 8191 rows
 // that the forward runs concurrently (measured: forward +0.9 % at batch 64,
 // the whole-batch launch 2 % slower with four).
 hipError_t launch_swiglu(const SwigluArgs& a, hipStream_t s) {
     if (a.rows < kSwigluSmallRows) return launch_swiglu_tiles<SwigluTileS, 2>(a, s);
-    return a.rows < 2 * kSwigluSmallRows ? launch_swiglu_tiles<SwigluTile, 4>(a, s) : launch_swiglu_tiles<SwigluTile, 2>(a, s);
+    return a.rows < kSwigluSplit4Rows ? launch_swiglu_tiles<SwigluTile, 4>(a, s) : launch_swiglu_tiles<SwigluTile, 2>(a, s);
 }
 
 hipError_t launch_splitk(const SplitKArgs& a, hipStream_t s) {
