@@ -151,8 +151,13 @@ void* scratch_address(int device) {
 // copies over.
 class Copier {
 public:
-    Copier() : worker_([this] { run(); }) {}
+    // threaded = false: submit() copies at once on the calling thread (one
+    // chunk has nothing to overlap, and a thread would only add its start).
+    explicit Copier(bool threaded) {
+        if (threaded) worker_ = std::thread([this] { run(); });
+    }
     ~Copier() {
+        if (!worker_.joinable()) return;
         {
             std::lock_guard<std::mutex> lock(m_);
             stop_ = true;
@@ -166,6 +171,11 @@ public:
     // Queues dst <- src (n bytes); returns the copy's ticket.
     uint64_t submit(void* dst, const void* src, uint64_t n) {
         std::lock_guard<std::mutex> lock(m_);
+        if (!worker_.joinable()) {
+            dhx::parallel_copy(dst, src, n);
+            ++done_;
+            return submitted_++;
+        }
         jobs_.push_back(Job{dst, src, n});
         work_.notify_all();
         return submitted_++;
@@ -202,7 +212,7 @@ private:
     std::deque<Job> jobs_;
     uint64_t submitted_ = 0, done_ = 0;
     bool stop_ = false;
-    std::thread worker_;  // last: starts once the members above exist
+    std::thread worker_;  // last: started (if threaded) once the members above exist
 };
 
 constexpr uint64_t align256(uint64_t v) { return (v + 255) & ~255ull; }
@@ -323,7 +333,7 @@ public:
         if (in_bytes(0) > dhx::engine_staging_in_bytes(e) || out_bytes(0) > dhx::engine_staging_out_bytes(e))
             throw Error("chunk exceeds reserved staging");
         std::vector<uint64_t> filled(chunks), drained(chunks);
-        Copier copier;
+        Copier copier(chunks > 1);
         // Chunk i's pixels into slot i % 2's input staging, once the slot's
         // previous upload has left it.
         auto fill = [&](uint64_t i) {
