@@ -312,11 +312,11 @@ public:
 
     // lib.rs:90-114: chunks of max_batch images, pipelined over the two
     // transfer slots: chunk i uses slot i % 2. This thread issues every HIP
-    // call (uploads, graph launches, readbacks) and a Copier thread does the
-    // host copies into and out of the pinned staging buffers, each handed
-    // over as soon as its buffer is free: chunk i+1's input copy and chunk
-    // i-1's output copy run while chunk i is launched and computed. Results
-    // are those of the chunks run one at a time.
+    // call (uploads, graph launches, readbacks); with more than one chunk a
+    // Copier thread does the host copies into and out of the pinned staging
+    // buffers, each handed over as soon as its buffer is free: chunk i+1's
+    // input copy and chunk i-1's output copy run while chunk i is launched
+    // and computed. Results are those of the chunks run one at a time.
     void forward(const float* pixels, uint64_t n, float* out, uint64_t out_floats) {
         check_input(pixels, n);
         const uint64_t batch = n / image_elems_;
