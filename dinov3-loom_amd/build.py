@@ -31,6 +31,7 @@ SOURCES = [
     "kernels/norm.hip",
     "engine.cpp",
     "model.cpp",
+    "host_copy.cpp",
     "weights.cpp",
     "safetensors.cpp",
 ]

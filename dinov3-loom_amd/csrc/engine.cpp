@@ -17,6 +17,7 @@
 #include "../../include/dinov3_engine.h"
 #include "engine_internal.hpp"
 #include "errors.hpp"
+#include "host_copy.hpp"
 #include "kernels/launch.hpp"
 
 namespace {
@@ -326,33 +327,6 @@ namespace dhx {
 
 // memcpy split over host threads: pageable <-> pinned copies of tens of MB
 // run at a few GB/s on one core, far below the PCIe link.
-void parallel_copy(void* dst, const void* src, uint64_t n) noexcept {
-    constexpr uint64_t kChunk = 4ull << 20;
-    const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
-    const unsigned threads = (unsigned)std::min<uint64_t>(std::min(16u, hw), (n + kChunk - 1) / kChunk);
-    if (threads <= 1) {
-        if (n) std::memcpy(dst, src, n);
-        return;
-    }
-    // Never throws: a thread that cannot be started leaves its part (and the
-    // parts after it) to the calling thread.
-    std::vector<std::thread> pool;
-    const uint64_t per = (n + threads - 1) / threads;
-    uint64_t handed = 0;  // bytes [0, handed) belong to started threads
-    try {
-        pool.reserve(threads);
-        for (unsigned t = 0; t < threads; ++t) {
-            const uint64_t a = t * per, b = std::min(n, a + per);
-            if (a >= b) break;
-            pool.emplace_back([=] { std::memcpy(static_cast<char*>(dst) + a, static_cast<const char*>(src) + a, b - a); });
-            handed = b;
-        }
-    } catch (...) {
-    }
-    if (handed < n) std::memcpy(static_cast<char*>(dst) + handed, static_cast<const char*>(src) + handed, n - handed);
-    for (auto& th : pool) th.join();
-}
-
 uint32_t engine_external(dhx_engine* e, void* ptr, uint64_t bytes) {
     e->buffers.push_back(ptr);
     e->sizes.push_back(bytes);

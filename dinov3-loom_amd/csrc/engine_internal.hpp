@@ -34,9 +34,6 @@ uint64_t engine_staging_out_bytes(const dhx_engine* e);
 void engine_wait_upload(dhx_engine* e, uint32_t slot);
 void engine_upload(dhx_engine* e, dhx_region dst, uint64_t n, uint32_t slot);
 void engine_wait_readback(dhx_engine* e, uint32_t slot);
-// memcpy split over up to 16 host threads; never throws (what no thread
-// can be started for is copied on the calling thread).
-void parallel_copy(void* dst, const void* src, uint64_t n) noexcept;
 // The engine's own stream and device.
 hipStream_t engine_stream(const dhx_engine* e);
 int engine_device(const dhx_engine* e);

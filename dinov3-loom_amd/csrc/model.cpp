@@ -5,10 +5,8 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
-#include <condition_variable>
 #include <cstdlib>
 #include <cstring>
-#include <deque>
 #include <map>
 #include <memory>
 #include <mutex>
@@ -20,6 +18,7 @@
 #include "../../include/dinov3.h"
 #include "engine_internal.hpp"
 #include "errors.hpp"
+#include "host_copy.hpp"
 #include "kernels/launch.hpp"
 #include "weights.hpp"
 
@@ -142,78 +141,6 @@ void* scratch_address(int device) {
     std::lock_guard<std::mutex> lock(g_scratch_mutex);
     return scratch_slot_locked(device).ptr;
 }
-
-// Host copies between pageable and pinned memory (each split over threads
-// by parallel_copy), run one after another on a thread of their own in the
-// order they are submitted. It never calls the HIP runtime: HIP calls from
-// another thread beside a graph launch were measured to slow the launch
-// down, so the thread that launches keeps every HIP call and hands the
-// copies over.
-class Copier {
-public:
-    // threaded = false: submit() copies at once on the calling thread (one
-    // chunk has nothing to overlap, and a thread would only add its start).
-    explicit Copier(bool threaded) {
-        if (threaded) worker_ = std::thread([this] { run(); });
-    }
-    ~Copier() {
-        if (!worker_.joinable()) return;
-        {
-            std::lock_guard<std::mutex> lock(m_);
-            stop_ = true;
-        }
-        work_.notify_all();
-        worker_.join();  // queued copies still run: their buffers outlive the caller's scope
-    }
-    Copier(const Copier&) = delete;
-    Copier& operator=(const Copier&) = delete;
-
-    // Queues dst <- src (n bytes); returns the copy's ticket.
-    uint64_t submit(void* dst, const void* src, uint64_t n) {
-        std::lock_guard<std::mutex> lock(m_);
-        if (!worker_.joinable()) {
-            dhx::parallel_copy(dst, src, n);
-            ++done_;
-            return submitted_++;
-        }
-        jobs_.push_back(Job{dst, src, n});
-        work_.notify_all();
-        return submitted_++;
-    }
-
-    // Waits until the copy with this ticket (and every earlier one) is done.
-    void wait(uint64_t ticket) {
-        std::unique_lock<std::mutex> lock(m_);
-        done_cv_.wait(lock, [&] { return done_ > ticket; });
-    }
-
-private:
-    struct Job {
-        void* dst;
-        const void* src;
-        uint64_t n;
-    };
-    void run() {
-        std::unique_lock<std::mutex> lock(m_);
-        for (;;) {
-            work_.wait(lock, [&] { return stop_ || !jobs_.empty(); });
-            if (jobs_.empty()) return;  // stopping, nothing left
-            const Job j = jobs_.front();
-            jobs_.pop_front();
-            lock.unlock();
-            dhx::parallel_copy(j.dst, j.src, j.n);
-            lock.lock();
-            ++done_;
-            done_cv_.notify_all();
-        }
-    }
-    std::mutex m_;
-    std::condition_variable work_, done_cv_;
-    std::deque<Job> jobs_;
-    uint64_t submitted_ = 0, done_ = 0;
-    bool stop_ = false;
-    std::thread worker_;  // last: started (if threaded) once the members above exist
-};
 
 constexpr uint64_t align256(uint64_t v) { return (v + 255) & ~255ull; }
 
