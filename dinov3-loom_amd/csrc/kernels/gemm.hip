@@ -18,6 +18,12 @@ using PatchTile = Tile<64, 128, 2, 2>;
 // LDS, not registers): four workgroups per CU, so a batch of 64 (909 tiles)
 // runs as one round of workgroups.
 using QkvTile = Tile<128, 128, 4, 1, 32>;
+// QKV for launches of fewer rows (batch 32's and 512x512 batch 8's image
+// groups, small batches): 128x64 tiles (one head per wave), twice the
+// workgroups. Same stage depth, and the LayerNorm fold is applied in the
+// epilogue, so a row's result is bitwise the same on either shape.
+using QkvTileS = Tile<128, 64, 4, 1, 32>;
+constexpr int kQkvSmallRows = 5120;
 using ResidTile = Tile<128, 64, 4, 1>;
 using ResidTileK = Tile<128, 64, 4, 1, 128>;  // down projection (k = 1536)
 using SwigluTile = Tile<256, 128, 4, 1, 64>;
@@ -52,13 +58,19 @@ hipError_t launch_patch_embed(const PatchEmbedArgs& a, hipStream_t s) {
                    : launch<PatchTile>(gemm::patch_embed_kernel<PatchTile, false>, tiles, a, s);
 }
 
-hipError_t launch_qkv_rope(const QkvArgs& a, hipStream_t s) {
-    const int tiles = tiles_for<QkvTile>(a.images * (a.grid * a.grid + kPrefix), 3 * kHidden);
+template <class T>
+static hipError_t launch_qkv_tiles(const QkvArgs& a, hipStream_t s) {
+    const int tiles = tiles_for<T>(a.images * (a.grid * a.grid + kPrefix), 3 * kHidden);
     const dim3 grid(gemm::tile_grid(tiles));
     const size_t lds = gemm::rope_lds_bytes(a.grid);
-    if (a.stats) hipLaunchKernelGGL((gemm::qkv_rope_kernel<QkvTile, true>), grid, dim3(QkvTile::THREADS), lds, s, a);
-    else hipLaunchKernelGGL((gemm::qkv_rope_kernel<QkvTile, false>), grid, dim3(QkvTile::THREADS), lds, s, a);
+    if (a.stats) hipLaunchKernelGGL((gemm::qkv_rope_kernel<T, true>), grid, dim3(T::THREADS), lds, s, a);
+    else hipLaunchKernelGGL((gemm::qkv_rope_kernel<T, false>), grid, dim3(T::THREADS), lds, s, a);
     return hipGetLastError();
+}
+
+hipError_t launch_qkv_rope(const QkvArgs& a, hipStream_t s) {
+    const int rows = a.images * (a.grid * a.grid + kPrefix);
+    return rows < kQkvSmallRows ? launch_qkv_tiles<QkvTileS>(a, s) : launch_qkv_tiles<QkvTile>(a, s);
 }
 
 hipError_t launch_resid(const ResidArgs& a, hipStream_t s) {

@@ -173,8 +173,8 @@ __device__ __forceinline__ void rope_table_dma(const float* cos, const float* si
     }
 }
 
-// QKV + bias + 2D RoPE. A wave's 128 columns are two heads of q, k or v (a
-// 128-column tile never straddles two of them); channel c and its rotation
+// QKV + bias + 2D RoPE. A wave's 64 or 128 columns are one or two heads of
+// q, k or v (a tile never straddles two of them); channel c and its rotation
 // partner c+32 of a head are acc.v[2h] / acc.v[2h+1] of the same lane, and
 // both use angle column c of the RoPE tables (DINOv3's tables repeat columns
 // 0..31 in 32..63; only the first half is read, from the LDS tables of
@@ -187,7 +187,9 @@ __device__ __forceinline__ void rope_table_dma(const float* cos, const float* si
 // per store instead). Launched with rope_lds_bytes(grid) of dynamic LDS.
 template <class T, bool LN>
 __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? (T::BK == 32 ? 4 : 3) : 2) void qkv_rope_kernel(QkvArgs p) {
-    static_assert(T::TN == 2 * kHeadDim && T::WGN == 1, "two heads per wave, whole rows per wave");
+    static_assert(T::TN % kHeadDim == 0 && kHidden % T::BN == 0 && T::WGN == 1,
+                  "whole heads per wave and tile, whole rows per wave");
+    static_assert(T::WAVES == 4, "four waves fill the four RoPE tables");
     __shared__ __attribute__((aligned(16))) half_t wb0[T::WF_HALFS], wb1[T::WF_HALFS], wb2[T::WF_HALFS];
     __shared__ __attribute__((aligned(16))) float cst[2][T::BN];  // bias, wsum of the tile's columns
     __shared__ float2_t rows_norm[T::BM];                          // (mean, rstd) of the tile's rows
@@ -273,7 +275,7 @@ __global__ __launch_bounds__(T::THREADS, T::FM == 1 ? (T::BK == 32 ? 4 : 3) : 2)
                 rn = RowNorm{v[0], v[1]};
             }
 #pragma unroll
-            for (int h2 = 0; h2 < 2; ++h2) {
+            for (int h2 = 0; h2 < T::TN / kHeadDim; ++h2) {
                 half4_t lo_h[4], up_h[4];
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {

@@ -227,7 +227,9 @@ def read_heads(e, region, images, tpad):
     return from_frag(e.read(region, np.float16, (n * 64,)), n, 64).reshape(images, 6, tpad, 64)
 
 
-@pytest.mark.parametrize("images,grid", [(3, 14), (1, 32), (2, 4)])
+# Launches under 5120 rows run 128x64 tiles, larger ones 128x128: (26, 14) is
+# 5226 rows.
+@pytest.mark.parametrize("images,grid", [(3, 14), (1, 32), (2, 4), (26, 14)])
 def test_qkv_rope(eng, images, grid):
     rng = np.random.default_rng(7 + grid)
     T = grid * grid + 5
@@ -478,7 +480,7 @@ def test_patch_embed_stats(eng, images, grid):
     check_stats(eng.read(st, np.float32, (images * T, 12)), y.reshape(-1, 384), "patch stats")
 
 
-@pytest.mark.parametrize("images,grid,offset", [(3, 14, 0.0), (1, 32, 0.5), (2, 14, 4.0)])
+@pytest.mark.parametrize("images,grid,offset", [(3, 14, 0.0), (1, 32, 0.5), (2, 14, 4.0), (26, 14, 0.5)])
 def test_qkv_rope_layernorm_fused(eng, images, grid, offset):
     rng = np.random.default_rng(grid * 7 + int(offset * 10))
     T = grid * grid + 5
